@@ -1,0 +1,145 @@
+/*
+ * leap_hip_attention — MI355X (gfx950) decode attention for the LEAP engine.
+ *
+ * Replaces the per-token attention block of the reference engine's layer
+ * step: RoPE on q and k, the key/value cache write, the GQA score pass,
+ * softmax and the weighted-V accumulation.  In the reference that block is
+ * inline code between the v projection and the wo projection:
+ *   src/inference/FloatTransformer.cpp:396-662   (fp32 engine)
+ *   src/inference/QuantizedTransformer.cpp:670-923 (int8 engine, same fp32 block)
+ * Entry state: the un-rotated q, k, v of one token for one layer.
+ * Exit state:  the head-major attention output (the reference's s->xb) and the
+ *              rotated k / plain v stored in cache[layer][pos].
+ *
+ * The key/value caches live in device memory with the reference's layout,
+ * one slab per sequence: [layer][pos][n_kv_heads*head_dim] fp32 (the
+ * reference's RunState key_cache/value_cache, FloatTransformer.cpp:50-51,
+ * offset l*seq_len*kv_dim + pos*kv_dim, :396-398), with 64-bit offsets.
+ *
+ * Conventions
+ *   - Every entry point returns 0 on success or a negative errno value:
+ *     -EINVAL bad argument, -ENOMEM allocation failure, -ENODEV no usable
+ *     GPU, -EIO a HIP runtime error.  The message of the last failure on a
+ *     handle is kept for leap_hip_attention_last_error.  Nothing throws across
+ *     this boundary.
+ *   - A handle is used by one host thread at a time; distinct handles are
+ *     independent.  Device work is ordered on a stream: the host-pointer
+ *     entry points use the handle's own stream and return when results are
+ *     in host memory; the _async entry points take device pointers and a
+ *     hipStream_t (0 = the default stream) and return after enqueueing.
+ *   - `layer` is the model's global layer index, as in the reference's layer
+ *     loop (FloatTransformer.cpp:768-770); a handle holds the layers
+ *     [layer_begin, layer_end).
+ */
+#ifndef LEAP_HIP_ATTENTION_H
+#define LEAP_HIP_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct leap_hip_attention leap_hip_attention;
+
+/* Model dimensions (the reference's Config, Config.h:5-13, restricted to what
+ * attention needs) plus the RoPE base, which the reference fixes at 500000
+ * (FloatTransformer.cpp:65) and its file header does not carry. */
+typedef struct leap_hip_attention_config {
+    int n_layers;    /* model layers (range check for `layer`)                 */
+    int layer_begin; /* first layer held by this handle                        */
+    int layer_end;   /* one past the last layer held                           */
+    int n_heads;     /* query heads                                            */
+    int n_kv_heads;  /* key/value heads; n_heads % n_kv_heads == 0             */
+    int head_dim;    /* dim / n_heads: 64 or 128                               */
+    int seq_len;     /* cache rows per layer (Config.seq_len)                  */
+    float rope_theta;/* 500000 in the reference; <= 0 selects 500000           */
+    int max_batch;   /* sequences (cache slabs) held; 1 for the engine         */
+    int device;      /* HIP device ordinal                                     */
+} leap_hip_attention_config;
+
+/* Allocates both caches (zeroed, as the reference's std::vector resize),
+ * builds the fp32 RoPE table on the host with the reference's formula
+ * (FloatTransformer.cpp:56-72) and uploads it, and allocates the split-K
+ * workspace.  Replaces init_run_state / precompute_freqs
+ * (FloatTransformer.cpp:39-72) for the attention state. */
+int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_attention **out);
+
+/* Frees everything the handle owns.  NULL is accepted. */
+int leap_hip_attention_destroy(leap_hip_attention *h);
+
+/* Message of the last failure on `h` ("" if none); with h == NULL, the last
+ * failure of leap_hip_attention_create on this thread. */
+const char *leap_hip_attention_last_error(const leap_hip_attention *h);
+
+/* One token, one layer, sequence 0 (FloatTransformer.cpp:396-662).
+ *   q     [n_heads*head_dim]   pre-RoPE query (the reference's s->q)
+ *   k_new [kv_dim]             pre-RoPE key of this token
+ *   v_new [kv_dim]             value of this token
+ *   out   [n_heads*head_dim]   attention output (the reference's s->xb)
+ * Host pointers; returns when `out` is written.  0 <= pos < seq_len. */
+int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const float *q,
+                            const float *k_new, const float *v_new, float *out);
+
+/* As leap_hip_attention_step, with device pointers, enqueued on `stream`. */
+int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, const float *q,
+                                  const float *k_new, const float *v_new, float *out,
+                                  void *stream);
+
+/* n_seq independent sequences (slabs 0..n_seq-1) at one layer, each at its
+ * own position pos[i] (ragged contexts).  Rows are [n_seq][...] with the
+ * per-sequence sizes of leap_hip_attention_step.  Host pointers.  The
+ * reference runs one sequence per engine; this is that step applied to a
+ * batch of engines' states. */
+int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq, const int *pos,
+                                    const float *q, const float *k_new, const float *v_new,
+                                    float *out);
+
+/* As leap_hip_attention_step_batched with device pointers (pos included),
+ * enqueued on `stream`.  max_pos is a host-side upper bound of pos[] used to
+ * size the launch; sequences whose pos lies outside [0, max_pos] or beyond
+ * seq_len are skipped and their outputs left unwritten. */
+int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int n_seq,
+                                          const int *pos, int max_pos, const float *q,
+                                          const float *k_new, const float *v_new, float *out,
+                                          void *stream);
+
+/* clear_kv_cache (FloatTransformer.cpp:74-77): zero both caches. */
+int leap_hip_attention_clear(leap_hip_attention *h);
+
+/* Copy cache rows [pos_begin, pos_end) of (seq, layer) between host memory
+ * and the device cache, in the reference's row layout ([pos][kv_dim]).
+ * Either k or v may be NULL to skip it.  Used for checkpoints, tests and to
+ * hand the same bytes to a CPU path. */
+int leap_hip_attention_kv_upload(leap_hip_attention *h, int seq, int layer, int pos_begin,
+                                 int pos_end, const float *k, const float *v);
+int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, int pos_begin,
+                                   int pos_end, float *k, float *v);
+
+/* ---- Extras with no counterpart in the reference ---------------------- */
+
+/* Fill every cache row of every held sequence and layer with seeded
+ * N(0,1)*scale values (SplitMix64 counter hash -> Box-Muller), on the device.
+ * Synthetic data for benchmarks and large tests. */
+int leap_hip_attention_kv_fill_normal(leap_hip_attention *h, uint64_t seed, float scale);
+
+/* Copy RoPE table rows [pos_begin, pos_end) to host memory as the reference
+ * holds them: cos and sin, each [pos][head_dim/2]. */
+int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int pos_end,
+                                     float *cos_out, float *sin_out);
+
+/* Positions per split-K chunk for later steps: 0 restores the automatic
+ * choice; otherwise a multiple of 64.  A tuning and test knob. */
+int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions);
+
+/* Device addresses of the (seq, layer) cache slabs, for callers that keep
+ * their own device-side views of the cache. */
+int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,
+                                     float **v);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEAP_HIP_ATTENTION_H */

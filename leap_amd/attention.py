@@ -1,0 +1,210 @@
+"""Python binding of the C-ABI in include/leap_hip_attention.h.
+
+``HipAttention`` owns one library handle: the device key/value caches in the
+reference engine's layout and the RoPE table.  Its methods map one-to-one to
+the C entry points and raise ``LeapError`` on a negative status, the way the
+reference engine raises ``std::runtime_error`` around its layer step.
+
+Host arrays are numpy float32; the ``*_async`` methods take raw device
+addresses (integers, e.g. ``tensor.data_ptr()``) and a raw ``hipStream_t``
+(``torch.cuda.Stream().cuda_stream``), so torch is plumbing only.
+"""
+from __future__ import annotations
+
+import ctypes
+import errno
+import os
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libleap_hip_attention.so")
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.c_int
+_P = ctypes.c_void_p
+
+EXPORTS = (
+    "leap_hip_attention_create", "leap_hip_attention_destroy", "leap_hip_attention_last_error",
+    "leap_hip_attention_step", "leap_hip_attention_step_async",
+    "leap_hip_attention_step_batched", "leap_hip_attention_step_batched_async",
+    "leap_hip_attention_clear", "leap_hip_attention_kv_upload", "leap_hip_attention_kv_download",
+    "leap_hip_attention_kv_fill_normal", "leap_hip_attention_rope_download",
+    "leap_hip_attention_set_split", "leap_hip_attention_kv_device_ptr",
+)
+
+
+class LeapError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        name = errno.errorcode.get(-code, str(code))
+        super().__init__(f"{msg} ({name})")
+        self.code = code
+
+
+class Config(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", _I), ("layer_begin", _I), ("layer_end", _I), ("n_heads", _I),
+        ("n_kv_heads", _I), ("head_dim", _I), ("seq_len", _I), ("rope_theta", ctypes.c_float),
+        ("max_batch", _I), ("device", _I),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load the HIP library; fails loudly when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.isfile(path):
+        raise RuntimeError(f"{path} is missing: build it with `python -m leap_amd.build`")
+    L = ctypes.CDLL(path)
+    H = _P
+    L.leap_hip_attention_create.argtypes = [ctypes.POINTER(Config), ctypes.POINTER(H)]
+    L.leap_hip_attention_destroy.argtypes = [H]
+    L.leap_hip_attention_last_error.argtypes = [H]
+    L.leap_hip_attention_last_error.restype = ctypes.c_char_p
+    L.leap_hip_attention_step.argtypes = [H, _I, _I, _F, _F, _F, _F]
+    L.leap_hip_attention_step_async.argtypes = [H, _I, _I, _P, _P, _P, _P, _P]
+    L.leap_hip_attention_step_batched.argtypes = [H, _I, _I, ctypes.POINTER(_I), _F, _F, _F, _F]
+    L.leap_hip_attention_step_batched_async.argtypes = [H, _I, _I, _P, _I, _P, _P, _P, _P, _P]
+    L.leap_hip_attention_clear.argtypes = [H]
+    L.leap_hip_attention_kv_upload.argtypes = [H, _I, _I, _I, _I, _F, _F]
+    L.leap_hip_attention_kv_download.argtypes = [H, _I, _I, _I, _I, _F, _F]
+    L.leap_hip_attention_kv_fill_normal.argtypes = [H, ctypes.c_uint64, ctypes.c_float]
+    L.leap_hip_attention_rope_download.argtypes = [H, _I, _I, _F, _F]
+    L.leap_hip_attention_set_split.argtypes = [H, _I]
+    L.leap_hip_attention_kv_device_ptr.argtypes = [H, _I, _I, ctypes.POINTER(_P),
+                                                   ctypes.POINTER(_P)]
+    for name in EXPORTS:
+        fn = getattr(L, name)
+        if name != "leap_hip_attention_last_error":
+            fn.restype = _I
+    _lib = L
+    return L
+
+
+def _fp(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a, n=None):
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    if n is not None and a.size != n:
+        raise ValueError(f"expected {n} floats, got {a.size}")
+    return a
+
+
+class HipAttention:
+    """One handle of the MI355X attention library (see the C header)."""
+
+    def __init__(self, n_heads, n_kv_heads, head_dim, seq_len, n_layers=1, layer_begin=0,
+                 layer_end=None, rope_theta=500000.0, max_batch=1, device=0):
+        self.lib = load_library()
+        self.cfg = Config(n_layers, layer_begin, n_layers if layer_end is None else layer_end,
+                          n_heads, n_kv_heads, head_dim, seq_len, rope_theta, max_batch, device)
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        self.seq_len, self.max_batch = seq_len, max_batch
+        self.q_dim, self.kv_dim = n_heads * head_dim, n_kv_heads * head_dim
+        h = _P()
+        rc = self.lib.leap_hip_attention_create(ctypes.byref(self.cfg), ctypes.byref(h))
+        if rc != 0:
+            raise LeapError(rc, self.lib.leap_hip_attention_last_error(None).decode())
+        self.h = h
+
+    # -- lifetime -----------------------------------------------------------
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.leap_hip_attention_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != 0:
+            raise LeapError(rc, self.lib.leap_hip_attention_last_error(self.h).decode())
+
+    # -- the step -----------------------------------------------------------
+    def step(self, layer, pos, q, k_new, v_new):
+        q, k, v = _f32(q, self.q_dim), _f32(k_new, self.kv_dim), _f32(v_new, self.kv_dim)
+        out = np.empty(self.q_dim, np.float32)
+        self._check(self.lib.leap_hip_attention_step(self.h, layer, pos, _fp(q), _fp(k), _fp(v),
+                                                     _fp(out)))
+        return out
+
+    def step_async(self, layer, pos, q_ptr, k_ptr, v_ptr, out_ptr, stream=0):
+        self._check(self.lib.leap_hip_attention_step_async(self.h, layer, pos, q_ptr, k_ptr,
+                                                           v_ptr, out_ptr, stream))
+
+    def step_batched(self, layer, pos, q, k_new, v_new):
+        pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(-1)
+        n = pos.size
+        q = _f32(q, n * self.q_dim)
+        k, v = _f32(k_new, n * self.kv_dim), _f32(v_new, n * self.kv_dim)
+        out = np.empty(n * self.q_dim, np.float32)
+        self._check(self.lib.leap_hip_attention_step_batched(
+            self.h, layer, n, pos.ctypes.data_as(ctypes.POINTER(_I)), _fp(q), _fp(k), _fp(v),
+            _fp(out)))
+        return out.reshape(n, self.q_dim)
+
+    def step_batched_async(self, layer, n_seq, pos_ptr, max_pos, q_ptr, k_ptr, v_ptr, out_ptr,
+                           stream=0):
+        self._check(self.lib.leap_hip_attention_step_batched_async(
+            self.h, layer, n_seq, pos_ptr, max_pos, q_ptr, k_ptr, v_ptr, out_ptr, stream))
+
+    # -- cache management ---------------------------------------------------
+    def clear(self):
+        self._check(self.lib.leap_hip_attention_clear(self.h))
+
+    def kv_upload(self, seq, layer, pos_begin, k=None, v=None):
+        rows = None
+        if k is not None:
+            k = _f32(k)
+            rows = k.size // self.kv_dim
+        if v is not None:
+            v = _f32(v)
+            rows = v.size // self.kv_dim if rows is None else rows
+        if rows is None:
+            return
+        self._check(self.lib.leap_hip_attention_kv_upload(self.h, seq, layer, pos_begin,
+                                                          pos_begin + rows, _fp(k), _fp(v)))
+
+    def kv_download(self, seq, layer, pos_begin, pos_end):
+        k = np.empty((pos_end - pos_begin, self.kv_dim), np.float32)
+        v = np.empty_like(k)
+        self._check(self.lib.leap_hip_attention_kv_download(self.h, seq, layer, pos_begin,
+                                                            pos_end, _fp(k), _fp(v)))
+        return k, v
+
+    def kv_fill_normal(self, seed, scale):
+        self._check(self.lib.leap_hip_attention_kv_fill_normal(self.h, seed, scale))
+
+    def rope_download(self, pos_begin=0, pos_end=None):
+        pos_end = self.seq_len if pos_end is None else pos_end
+        c = np.empty((pos_end - pos_begin, self.head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        self._check(self.lib.leap_hip_attention_rope_download(self.h, pos_begin, pos_end,
+                                                              _fp(c), _fp(s)))
+        return c, s
+
+    def set_split(self, chunk_positions):
+        self._check(self.lib.leap_hip_attention_set_split(self.h, chunk_positions))
+
+    def kv_device_ptr(self, seq, layer):
+        k, v = _P(), _P()
+        self._check(self.lib.leap_hip_attention_kv_device_ptr(self.h, seq, layer,
+                                                              ctypes.byref(k), ctypes.byref(v)))
+        return k.value, v.value

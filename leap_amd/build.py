@@ -1,0 +1,66 @@
+"""Build recipe for libleap_hip_attention.so (gfx950), in-tree.
+
+    python -m leap_amd.build
+
+The RoPE table TU is compiled by the host C++ compiler with the reference's
+release flags; the HIP TU by hipcc for gfx950 only.  Packed-fp32 VALU
+instructions are disabled for device code (``-packed-fp32-ops``).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+BUILD = os.path.join(ROOT, "_build")
+LIB = os.path.join(PKG, "libleap_hip_attention.so")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-ffp-contract=fast",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed: {' '.join(cmd)}")
+    return r
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    rope_o = os.path.join(BUILD, "rope_table.o")
+    hip_o = os.path.join(BUILD, "leap_hip_attention.o")
+    steps = [
+        ["g++", "-std=c++17", "-O3", "-march=x86-64-v3", "-ffast-math", "-fPIC", "-c",
+         os.path.join(CSRC, "rope_table.cpp"), "-o", rope_o],
+        [_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
+         os.path.join(CSRC, "leap_hip_attention.hip"), "-o", hip_o],
+        [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", hip_o, rope_o],
+    ]
+    for cmd in steps:
+        if verbose:
+            print(" ".join(cmd))
+        _run(cmd)
+    os.replace(LIB + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

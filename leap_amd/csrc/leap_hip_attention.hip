@@ -1,0 +1,460 @@
+// C-ABI of the MI355X decode-attention library (include/leap_hip_attention.h).
+//
+// Host side: argument checks, device allocations in the reference's cache
+// layout, the RoPE table upload, launch sizing for the split-K kernel, and the
+// host<->device copies of the synchronous entry points.  Device side:
+// decode_attention.hpp.
+#include "leap_hip_attention.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cerrno>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "decode_attention.hpp"
+
+extern "C" void leap_rope_table_host(int seq_len, int head_size, float theta, float *cos_tab,
+                                     float *sin_tab);
+
+struct leap_hip_attention {
+    leap_hip_attention_config cfg{};
+    int n_local = 0;          // layers held
+    int kv_dim = 0, q_dim = 0, group = 0;
+    size_t layer_floats = 0;  // seq_len * kv_dim
+    size_t slab_floats = 0;   // n_local * layer_floats, one sequence
+    float *k_cache = nullptr, *v_cache = nullptr;
+    float4 *rope = nullptr;
+    float *ws_o = nullptr;
+    float2 *ws_ml = nullptr;
+    int *counters = nullptr;
+    int *pos_dev = nullptr;
+    float *q_dev = nullptr, *k_dev = nullptr, *v_dev = nullptr, *out_dev = nullptr;
+    hipStream_t stream = nullptr;
+    int split = 0;
+    std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_error;
+
+int set_err(leap_hip_attention *h, int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (h)
+        h->err = buf;
+    else
+        g_create_error = buf;
+    return code;
+}
+
+#define HIP_TRY(h, call)                                                                       \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return set_err((h), e_ == hipErrorOutOfMemory ? -ENOMEM : -EIO, "%s: %s", #call,  \
+                           hipGetErrorString(e_));                                             \
+    } while (0)
+
+using KernelFn = void (*)(leap::StepArgs);
+
+KernelFn pick_kernel(int hd, int g)
+{
+#define LEAP_CASE(HD, G) \
+    if (hd == HD && g == G) return leap::decode_attention_kernel<HD, G>;
+    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+#undef LEAP_CASE
+    return nullptr;
+}
+
+int check_layer(leap_hip_attention *h, int layer)
+{
+    if (layer < h->cfg.layer_begin || layer >= h->cfg.layer_end)
+        return set_err(h, -EINVAL, "layer %d outside the held range [%d, %d)", layer,
+                       h->cfg.layer_begin, h->cfg.layer_end);
+    return 0;
+}
+
+int round_up(int x, int q) { return (x + q - 1) / q * q; }
+
+// Positions per workgroup: enough workgroups to keep every CU streaming
+// (about 1024 over the launch), at least one quantum, and at most kMaxChunks
+// chunks per sequence.
+int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
+{
+    const int quantum = leap::rows_per_pass(h->cfg.head_dim);
+    const int floor_chunk = round_up((max_T + leap::kMaxChunks - 1) / leap::kMaxChunks, quantum);
+    int c;
+    if (h->split > 0) {
+        c = round_up(h->split, quantum);
+    } else {
+        const long long target_wgs = 1024;
+        long long per = (total_rows * h->cfg.n_kv_heads + target_wgs - 1) / target_wgs;
+        per = std::min<long long>(per, 1 << 20);
+        c = round_up((int)per, quantum);
+    }
+    return std::max(c, std::max(floor_chunk, quantum));
+}
+
+int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
+           int max_pos, long long total_rows, const float *q, const float *k, const float *v,
+           float *out, hipStream_t stream)
+{
+    const int hd = h->cfg.head_dim;
+    KernelFn fn = pick_kernel(hd, h->group);
+    if (!fn) return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", hd, h->group);
+    const int chunk = choose_chunk(h, total_rows, max_pos + 1);
+    const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
+
+    leap::StepArgs a{};
+    a.q = q;
+    a.k_new = k;
+    a.v_new = v;
+    a.out = out;
+    const size_t loff = (size_t)(layer - h->cfg.layer_begin) * h->layer_floats;
+    a.k_cache = h->k_cache + loff;
+    a.v_cache = h->v_cache + loff;
+    a.rope = h->rope;
+    a.pos_dev = pos_dev;
+    a.ws_o = h->ws_o;
+    a.ws_ml = h->ws_ml;
+    a.counters = h->counters;
+    a.seq_stride = (long long)h->slab_floats;
+    a.pos_scalar = pos_scalar;
+    a.max_pos = max_pos;
+    a.seq_len = h->cfg.seq_len;
+    a.n_heads = h->cfg.n_heads;
+    a.n_kv_heads = h->cfg.n_kv_heads;
+    a.chunk = chunk;
+    a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
+
+    hipLaunchKernelGGL(fn, dim3(grid_x, h->cfg.n_kv_heads, n_seq), dim3(leap::kThreads), 0,
+                       stream, a);
+    HIP_TRY(h, hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_attention **out)
+{
+    if (!out) return set_err(nullptr, -EINVAL, "out is NULL");
+    *out = nullptr;
+    if (!cfg) return set_err(nullptr, -EINVAL, "cfg is NULL");
+    const leap_hip_attention_config c = *cfg;
+    if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0)
+        return set_err(nullptr, -EINVAL, "n_heads %d must be a positive multiple of n_kv_heads %d",
+                       c.n_heads, c.n_kv_heads);
+    if (!pick_kernel(c.head_dim, c.n_heads / c.n_kv_heads))
+        return set_err(nullptr, -EINVAL, "unsupported head_dim %d with %d q heads per kv head",
+                       c.head_dim, c.n_heads / c.n_kv_heads);
+    if (c.seq_len <= 0 || c.n_layers <= 0 || c.layer_begin < 0 || c.layer_end > c.n_layers ||
+        c.layer_begin >= c.layer_end)
+        return set_err(nullptr, -EINVAL, "bad layer range [%d, %d) of %d or seq_len %d",
+                       c.layer_begin, c.layer_end, c.n_layers, c.seq_len);
+    if (c.max_batch <= 0 || c.max_batch > 65535)
+        return set_err(nullptr, -EINVAL, "max_batch %d out of range", c.max_batch);
+    if (!(c.rope_theta <= 0.0f || std::isfinite(c.rope_theta)))
+        return set_err(nullptr, -EINVAL, "rope_theta must be finite");
+
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return set_err(nullptr, -ENODEV, "no HIP device");
+    if (c.device < 0 || c.device >= ndev)
+        return set_err(nullptr, -EINVAL, "device %d of %d", c.device, ndev);
+
+    leap_hip_attention *h = new (std::nothrow) leap_hip_attention;
+    if (!h) return set_err(nullptr, -ENOMEM, "host allocation failed");
+    h->cfg = c;
+    if (h->cfg.rope_theta <= 0.0f) h->cfg.rope_theta = 500000.0f;
+    h->n_local = c.layer_end - c.layer_begin;
+    h->kv_dim = c.n_kv_heads * c.head_dim;
+    h->q_dim = c.n_heads * c.head_dim;
+    h->group = c.n_heads / c.n_kv_heads;
+    h->layer_floats = (size_t)c.seq_len * h->kv_dim;
+    h->slab_floats = (size_t)h->n_local * h->layer_floats;
+
+    auto fail = [&](int rc) {
+        g_create_error = h->err;
+        leap_hip_attention_destroy(h);
+        return rc;
+    };
+    int rc;
+#define CREATE_TRY(call)                                   \
+    do {                                                   \
+        if ((rc = [&]() -> int { HIP_TRY(h, call); return 0; }()) != 0) return fail(rc); \
+    } while (0)
+
+    CREATE_TRY(hipSetDevice(c.device));
+    CREATE_TRY(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+    const size_t cache_bytes = (size_t)c.max_batch * h->slab_floats * sizeof(float);
+    CREATE_TRY(hipMalloc(&h->k_cache, cache_bytes));
+    CREATE_TRY(hipMalloc(&h->v_cache, cache_bytes));
+    CREATE_TRY(hipMemsetAsync(h->k_cache, 0, cache_bytes, h->stream));
+    CREATE_TRY(hipMemsetAsync(h->v_cache, 0, cache_bytes, h->stream));
+
+    const size_t rope_n = (size_t)c.seq_len * (c.head_dim / 2);
+    std::vector<float> cs(rope_n), sn(rope_n);
+    leap_rope_table_host(c.seq_len, c.head_dim, h->cfg.rope_theta, cs.data(), sn.data());
+    std::vector<float> packed(2 * rope_n);  // (cos, sin) per pair
+    for (size_t i = 0; i < rope_n; i++) {
+        packed[2 * i] = cs[i];
+        packed[2 * i + 1] = sn[i];
+    }
+    CREATE_TRY(hipMalloc(&h->rope, packed.size() * sizeof(float)));
+    CREATE_TRY(hipMemcpyAsync(h->rope, packed.data(), packed.size() * sizeof(float),
+                              hipMemcpyHostToDevice, h->stream));
+
+    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::kMaxChunks;
+    CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
+    const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads;
+    CREATE_TRY(hipMalloc(&h->counters, n_ctr * sizeof(int)));
+    CREATE_TRY(hipMemsetAsync(h->counters, 0, n_ctr * sizeof(int), h->stream));
+    CREATE_TRY(hipMalloc(&h->pos_dev, (size_t)c.max_batch * sizeof(int)));
+    CREATE_TRY(hipMalloc(&h->q_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->out_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->k_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->v_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
+    CREATE_TRY(hipStreamSynchronize(h->stream));
+#undef CREATE_TRY
+    *out = h;
+    return 0;
+}
+
+int leap_hip_attention_destroy(leap_hip_attention *h)
+{
+    if (!h) return 0;
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
+    void *bufs[] = {h->k_cache, h->v_cache, h->rope, h->ws_o, h->ws_ml, h->counters,
+                    h->pos_dev, h->q_dev, h->k_dev, h->v_dev, h->out_dev};
+    for (void *p : bufs)
+        if (p) (void)hipFree(p);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
+    delete h;
+    return 0;
+}
+
+const char *leap_hip_attention_last_error(const leap_hip_attention *h)
+{
+    return h ? h->err.c_str() : g_create_error.c_str();
+}
+
+int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, const float *q,
+                                  const float *k_new, const float *v_new, float *out,
+                                  void *stream)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (pos < 0 || pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
+    if (!q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    return launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k_new, v_new, out,
+                  (hipStream_t)stream);
+}
+
+int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const float *q,
+                            const float *k_new, const float *v_new, float *out)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (pos < 0 || pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
+    if (!q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    hipStream_t s = h->stream;
+    HIP_TRY(h, hipMemcpyAsync(h->q_dev, q, h->q_dim * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->k_dev, k_new, h->kv_dim * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->v_dev, v_new, h->kv_dim * sizeof(float), hipMemcpyHostToDevice, s));
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, h->q_dev, h->k_dev, h->v_dev,
+                        h->out_dev, s))
+        return rc;
+    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, h->q_dim * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    return 0;
+}
+
+int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int n_seq,
+                                          const int *pos, int max_pos, const float *q,
+                                          const float *k_new, const float *v_new, float *out,
+                                          void *stream)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (n_seq <= 0 || n_seq > h->cfg.max_batch)
+        return set_err(h, -EINVAL, "n_seq %d outside [1, %d]", n_seq, h->cfg.max_batch);
+    if (max_pos < 0 || max_pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "max_pos %d outside [0, %d)", max_pos, h->cfg.seq_len);
+    if (!pos || !q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    // Without the host positions, size the chunks as if every sequence were
+    // half the longest.
+    const long long rows = (long long)n_seq * (max_pos + 1) / 2 + 1;
+    return launch(h, layer, n_seq, pos, 0, max_pos, rows, q, k_new, v_new, out,
+                  (hipStream_t)stream);
+}
+
+int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq, const int *pos,
+                                    const float *q, const float *k_new, const float *v_new,
+                                    float *out)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (n_seq <= 0 || n_seq > h->cfg.max_batch)
+        return set_err(h, -EINVAL, "n_seq %d outside [1, %d]", n_seq, h->cfg.max_batch);
+    if (!pos || !q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    int max_pos = 0;
+    long long rows = 0;
+    for (int i = 0; i < n_seq; i++) {
+        if (pos[i] < 0 || pos[i] >= h->cfg.seq_len)
+            return set_err(h, -EINVAL, "pos[%d] = %d outside [0, %d)", i, pos[i], h->cfg.seq_len);
+        max_pos = std::max(max_pos, pos[i]);
+        rows += pos[i] + 1;
+    }
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    hipStream_t s = h->stream;
+    HIP_TRY(h, hipMemcpyAsync(h->pos_dev, pos, n_seq * sizeof(int), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->q_dev, q, (size_t)n_seq * h->q_dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->k_dev, k_new, (size_t)n_seq * h->kv_dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->v_dev, v_new, (size_t)n_seq * h->kv_dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    if (int rc = launch(h, layer, n_seq, h->pos_dev, 0, max_pos, rows, h->q_dev, h->k_dev,
+                        h->v_dev, h->out_dev, s))
+        return rc;
+    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, (size_t)n_seq * h->q_dim * sizeof(float),
+                              hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    return 0;
+}
+
+int leap_hip_attention_clear(leap_hip_attention *h)
+{
+    if (!h) return -EINVAL;
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    const size_t bytes = (size_t)h->cfg.max_batch * h->slab_floats * sizeof(float);
+    HIP_TRY(h, hipMemsetAsync(h->k_cache, 0, bytes, h->stream));
+    HIP_TRY(h, hipMemsetAsync(h->v_cache, 0, bytes, h->stream));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+static int kv_range(leap_hip_attention *h, int seq, int layer, int pos_begin, int pos_end,
+                    size_t *off, size_t *n)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (seq < 0 || seq >= h->cfg.max_batch)
+        return set_err(h, -EINVAL, "seq %d outside [0, %d)", seq, h->cfg.max_batch);
+    if (pos_begin < 0 || pos_end > h->cfg.seq_len || pos_begin > pos_end)
+        return set_err(h, -EINVAL, "position range [%d, %d) outside [0, %d)", pos_begin, pos_end,
+                       h->cfg.seq_len);
+    *off = (size_t)seq * h->slab_floats + (size_t)(layer - h->cfg.layer_begin) * h->layer_floats +
+           (size_t)pos_begin * h->kv_dim;
+    *n = (size_t)(pos_end - pos_begin) * h->kv_dim;
+    return 0;
+}
+
+int leap_hip_attention_kv_upload(leap_hip_attention *h, int seq, int layer, int pos_begin,
+                                 int pos_end, const float *k, const float *v)
+{
+    size_t off, n;
+    if (int rc = kv_range(h, seq, layer, pos_begin, pos_end, &off, &n)) return rc;
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    if (n == 0) return 0;
+    if (k) HIP_TRY(h, hipMemcpyAsync(h->k_cache + off, k, n * sizeof(float), hipMemcpyHostToDevice, h->stream));
+    if (v) HIP_TRY(h, hipMemcpyAsync(h->v_cache + off, v, n * sizeof(float), hipMemcpyHostToDevice, h->stream));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, int pos_begin,
+                                   int pos_end, float *k, float *v)
+{
+    size_t off, n;
+    if (int rc = kv_range(h, seq, layer, pos_begin, pos_end, &off, &n)) return rc;
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    if (n == 0) return 0;
+    if (k) HIP_TRY(h, hipMemcpyAsync(k, h->k_cache + off, n * sizeof(float), hipMemcpyDeviceToHost, h->stream));
+    if (v) HIP_TRY(h, hipMemcpyAsync(v, h->v_cache + off, n * sizeof(float), hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int leap_hip_attention_kv_fill_normal(leap_hip_attention *h, uint64_t seed, float scale)
+{
+    if (!h) return -EINVAL;
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    const size_t n = (size_t)h->cfg.max_batch * h->slab_floats;
+    const int blocks = 256 * 16;
+    hipLaunchKernelGGL(leap::fill_normal_kernel, dim3(blocks), dim3(256), 0, h->stream,
+                       h->k_cache, n, seed, scale);
+    HIP_TRY(h, hipGetLastError());
+    hipLaunchKernelGGL(leap::fill_normal_kernel, dim3(blocks), dim3(256), 0, h->stream,
+                       h->v_cache, n, seed ^ 0x5DEECE66DA3B9F21ull, scale);
+    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    return 0;
+}
+
+int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int pos_end,
+                                     float *cos_out, float *sin_out)
+{
+    if (!h) return -EINVAL;
+    if (pos_begin < 0 || pos_end > h->cfg.seq_len || pos_begin > pos_end)
+        return set_err(h, -EINVAL, "position range [%d, %d) outside [0, %d)", pos_begin, pos_end,
+                       h->cfg.seq_len);
+    if (!cos_out || !sin_out) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    const size_t half = h->cfg.head_dim / 2;
+    const size_t n = (size_t)(pos_end - pos_begin) * half;
+    if (n == 0) return 0;
+    std::vector<float> packed(2 * n);
+    HIP_TRY(h, hipMemcpyAsync(packed.data(),
+                              reinterpret_cast<float *>(h->rope) + 2 * (size_t)pos_begin * half,
+                              packed.size() * sizeof(float), hipMemcpyDeviceToHost, h->stream));
+    HIP_TRY(h, hipStreamSynchronize(h->stream));
+    for (size_t i = 0; i < n; i++) {
+        cos_out[i] = packed[2 * i];
+        sin_out[i] = packed[2 * i + 1];
+    }
+    return 0;
+}
+
+int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions)
+{
+    if (!h) return -EINVAL;
+    if (chunk_positions < 0 || chunk_positions % 64 != 0)
+        return set_err(h, -EINVAL, "chunk %d is not a non-negative multiple of 64",
+                       chunk_positions);
+    h->split = chunk_positions;
+    return 0;
+}
+
+int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,
+                                     float **v)
+{
+    size_t off, n;
+    if (int rc = kv_range(h, seq, layer, 0, 0, &off, &n)) return rc;
+    if (k) *k = h->k_cache + off;
+    if (v) *v = h->v_cache + off;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,164 @@
+"""ORACLE — test infrastructure only.
+
+ctypes bindings for the CPU restatement (``liboracle_attn.so``, built from
+``attn_oracle.c``) and for the driver around the reference's own code
+(``_ref/libleap_ref.so``, built from ``ref_harness.cpp`` plus the reference's
+``src/inference/FloatTransformer.cpp``).  Only the tests, the smoke check and
+the CPU-baseline leg of the benchmark import this module; the product package
+``leap_amd`` never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle_attn.so")
+REF_SO = os.path.join(HERE, "_ref", "libleap_ref.so")
+REF_SRC = "/root/reference/src/inference"
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.c_int
+
+
+def build(ref: bool | None = None) -> None:
+    """Compile the restatement, and the reference driver when the reference
+    sources are present (they are not on machines that only run prebuilt
+    libraries)."""
+    targets = ["all"]
+    if ref is None:
+        ref = os.path.isfile(os.path.join(REF_SRC, "FloatTransformer.cpp"))
+    if ref:
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-B", "-C", HERE] + targets, check=True)
+
+
+def _fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.isfile(ORACLE_SO):
+            raise RuntimeError(f"oracle library missing: {ORACLE_SO} (run oracle.build())")
+        L = ctypes.CDLL(ORACLE_SO)
+        L.oracle_rope_table.argtypes = [_I, _I, ctypes.c_float, _F, _F]
+        L.oracle_rope_table.restype = None
+        step_args = [_I, _I, _I, _I, _I, _I, _F, _F, _F, _F, _F, _F, _F, _F, _F]
+        L.oracle_attention_step.argtypes = step_args
+        L.oracle_attention_step.restype = _I
+        L.oracle_attention_step_mutant.argtypes = [_I] + step_args
+        L.oracle_attention_step_mutant.restype = _I
+        L.oracle_clear.argtypes = [_F, _F, ctypes.c_size_t]
+        L.oracle_set_threads.argtypes = [_I]
+        L.oracle_max_threads.restype = _I
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.isfile(REF_SO)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"reference driver missing: {REF_SO}")
+        L = ctypes.CDLL(REF_SO)
+        L.leapref_rope_table.argtypes = [_I, _I, _I, _F, _F]
+        L.leapref_rope_table.restype = _I
+        L.leapref_run_layer.argtypes = [_I] * 7 + [_F] * 10
+        L.leapref_run_layer.restype = _I
+        L.leapref_clear_check.argtypes = [_I] * 5
+        L.leapref_clear_check.restype = ctypes.c_long
+        _ref = L
+    return _ref
+
+
+def rope_table(seq_len: int, head_dim: int, theta: float = 500000.0):
+    """FloatTransformer.cpp:56-72 -> (cos, sin), each [seq_len, head_dim/2] fp32."""
+    c = np.empty((seq_len, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    lib().oracle_rope_table(seq_len, head_dim, theta, _fp(c), _fp(s))
+    return c, s
+
+
+class Oracle:
+    """One sequence's reference-layout cache plus the restated step.
+
+    ``key_cache``/``value_cache`` are ``[n_layers, seq_len, kv_dim]`` fp32,
+    exactly the reference's RunState layout (FloatTransformer.cpp:50-51).
+    """
+
+    def __init__(self, n_layers, n_heads, n_kv_heads, head_dim, seq_len, theta=500000.0,
+                 rope=None):
+        self.n_layers, self.n_heads, self.n_kv_heads = n_layers, n_heads, n_kv_heads
+        self.head_dim, self.seq_len, self.theta = head_dim, seq_len, theta
+        self.kv_dim = n_kv_heads * head_dim
+        self.key_cache = np.zeros((n_layers, seq_len, self.kv_dim), np.float32)
+        self.value_cache = np.zeros_like(self.key_cache)
+        if rope is None:
+            rope = rope_table(seq_len, head_dim, theta)
+        self.cos, self.sin = (np.ascontiguousarray(r, np.float32) for r in rope)
+
+    def step(self, layer, pos, q, k_new, v_new, mutant: int = 0):
+        """Returns (out [n_heads*hd], q rotated).  Updates the cache slot."""
+        q = np.array(q, np.float32, copy=True).reshape(-1)
+        k_new = np.ascontiguousarray(k_new, np.float32).reshape(-1)
+        v_new = np.ascontiguousarray(v_new, np.float32).reshape(-1)
+        att = np.empty(self.n_heads * (pos + 1), np.float32)
+        out = np.empty(self.n_heads * self.head_dim, np.float32)
+        args = (self.n_heads, self.n_kv_heads, self.head_dim, self.seq_len, layer, pos,
+                _fp(self.key_cache), _fp(self.value_cache), _fp(self.cos), _fp(self.sin),
+                _fp(q), _fp(k_new), _fp(v_new), _fp(att), _fp(out))
+        if mutant:
+            rc = lib().oracle_attention_step_mutant(mutant, *args)
+        else:
+            rc = lib().oracle_attention_step(*args)
+        if rc != 0:
+            raise ValueError("oracle_attention_step rejected its arguments")
+        return out, q
+
+    def clear(self):
+        lib().oracle_clear(_fp(self.key_cache), _fp(self.value_cache), self.key_cache.size)
+
+
+def ref_run_layer(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, wq, wk, wv,
+                  key_cache, value_cache):
+    """Run the reference's run_layer; returns dict with q_pre, k_pre, v_pre,
+    q_rot, out and the updated caches (copies)."""
+    hd = dim // n_heads
+    kv_dim = n_kv_heads * hd
+    kc = np.array(key_cache, np.float32, copy=True)
+    vc = np.array(value_cache, np.float32, copy=True)
+    outs = {k: np.empty(n, np.float32) for k, n in
+            (("q_pre", dim), ("k_pre", kv_dim), ("v_pre", kv_dim), ("q_rot", dim), ("out", dim))}
+    rc = ref().leapref_run_layer(
+        dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos,
+        _fp(np.ascontiguousarray(x, np.float32)), _fp(np.ascontiguousarray(wq, np.float32)),
+        _fp(np.ascontiguousarray(wk, np.float32)), _fp(np.ascontiguousarray(wv, np.float32)),
+        _fp(kc), _fp(vc), _fp(outs["q_pre"]), _fp(outs["k_pre"]), _fp(outs["v_pre"]),
+        _fp(outs["q_rot"]), _fp(outs["out"]))
+    if rc != 0:
+        raise RuntimeError("reference run_layer failed")
+    outs["key_cache"], outs["value_cache"] = kc, vc
+    return outs
+
+
+def ref_rope_table(dim, n_heads, seq_len):
+    hd = dim // n_heads
+    c = np.empty((seq_len, hd // 2), np.float32)
+    s = np.empty_like(c)
+    if ref().leapref_rope_table(dim, n_heads, seq_len, _fp(c), _fp(s)) != 0:
+        raise RuntimeError("reference rope table failed")
+    return c, s

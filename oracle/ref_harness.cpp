@@ -1,0 +1,161 @@
+// ORACLE — test infrastructure only.
+//
+// A thin C driver around the reference's own FloatTransformer, compiled
+// together with the reference source file where it lies (see
+// oracle/Makefile); the product never links it.  It runs the reference's
+// run_layer (src/inference/FloatTransformer.cpp:384-749) on synthetic state so
+// the restatement in attn_oracle.c can be checked against the real code.
+//
+// How the attention block is isolated: the layer is given wo = identity,
+// rms weights = 1 and zero FFN weights (hidden_dim may be tiny), so
+//   s->xb2 = wo . xb = the attention output exactly (an identity GEMV adds
+//            one product x*1 to zeros), and
+//   cache[l][pos] holds the rotated k after the call.
+// The pre-RoPE q, k, v are produced by the reference's own rmsnorm and matmul
+// on the same inputs, computed here once before run_layer with the same
+// deterministic functions (rmsnorm has no threading, matmul is a static
+// OpenMP schedule with one owner per output row).
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <iostream>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+#include <sys/mman.h>
+
+// run_layer, rmsnorm, matmul and the run state are private members of the
+// reference class; this test driver opens them up for itself only.
+#define private public
+#include "FloatTransformer.h"
+#undef private
+
+using Inference::Config;
+using Inference::FloatTransformer;
+
+namespace {
+
+struct Weights {
+    std::vector<float> buf;
+};
+
+// Lay out a weight blob in the order FloatTransformer::memory_map_weights
+// carves it (FloatTransformer.cpp:947-978) for one layer, with rms weights 1,
+// wq/wk/wv given, wo = identity and zero FFN/embedding/classifier.
+std::unique_ptr<FloatTransformer> make_engine(const Config &c, const float *wq, const float *wk,
+                                              const float *wv, int layer, Weights &w)
+{
+    const size_t dim = c.dim, L = c.n_layers, hd = c.dim / c.n_heads;
+    const size_t kv_dim = (size_t)c.n_kv_heads * hd;
+    const size_t n_att = L * dim, n_ffn = L * dim, n_fin = dim, n_emb = (size_t)c.vocab_size * dim;
+    const size_t n_wq = L * dim * dim, n_wk = L * dim * kv_dim, n_wv = n_wk, n_wo = L * dim * dim;
+    const size_t n_w1 = L * dim * c.hidden_dim, n_w2 = n_w1, n_w3 = n_w1;
+    w.buf.assign(n_att + n_ffn + n_fin + n_emb + n_wq + n_wk + n_wv + n_wo + n_w1 + n_w2 + n_w3, 0.0f);
+    float *p = w.buf.data();
+    std::fill(p, p + n_att + n_ffn + n_fin, 1.0f);
+    float *pwq = p + n_att + n_ffn + n_fin + n_emb;
+    float *pwk = pwq + n_wq;
+    float *pwv = pwk + n_wk;
+    float *pwo = pwv + n_wv;
+    std::memcpy(pwq + (size_t)layer * dim * dim, wq, sizeof(float) * dim * dim);
+    std::memcpy(pwk + (size_t)layer * dim * kv_dim, wk, sizeof(float) * dim * kv_dim);
+    std::memcpy(pwv + (size_t)layer * dim * kv_dim, wv, sizeof(float) * dim * kv_dim);
+    float *wo_l = pwo + (size_t)layer * dim * dim;
+    for (size_t i = 0; i < dim; i++) wo_l[i * dim + i] = 1.0f;
+    return std::make_unique<FloatTransformer>(c, -1, MAP_FAILED, 0, w.buf.data(), 1);
+}
+
+Config make_config(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len)
+{
+    Config c{};
+    c.dim = dim;
+    c.hidden_dim = 8;
+    c.n_layers = n_layers;
+    c.n_heads = n_heads;
+    c.n_kv_heads = n_kv_heads;
+    c.vocab_size = 1;
+    c.seq_len = seq_len;
+    return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+// The reference's RoPE tables (precompute_freqs, FloatTransformer.cpp:56-72).
+int leapref_rope_table(int dim, int n_heads, int seq_len, float *cos_out, float *sin_out)
+{
+    try {
+        Config c = make_config(dim, n_heads, n_heads, 1, seq_len);
+        const size_t hd = dim / n_heads;
+        std::vector<float> wq((size_t)dim * dim), wk((size_t)dim * dim), wv((size_t)dim * dim);
+        Weights w;
+        auto eng = make_engine(c, wq.data(), wk.data(), wv.data(), 0, w);
+        std::memcpy(cos_out, eng->rope_cos.data(), sizeof(float) * (size_t)seq_len * (hd / 2));
+        std::memcpy(sin_out, eng->rope_sin.data(), sizeof(float) * (size_t)seq_len * (hd / 2));
+        return 0;
+    } catch (const std::exception &e) {
+        std::cerr << "leapref_rope_table: " << e.what() << "\n";
+        return -1;
+    }
+}
+
+// Run the reference run_layer(layer, pos, x) once.
+//   key_cache/value_cache: [n_layers][seq_len][kv_dim], in: prior state,
+//                          out: the reference's state after the call
+//   q_pre/k_pre/v_pre:     out, the pre-RoPE projections run_layer computes
+//   q_rot:                 out, s->q after the call (rotated q)
+//   att_out:               out, s->xb (head-major attention output)
+int leapref_run_layer(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len, int layer,
+                      int pos, const float *x_in, const float *wq, const float *wk, const float *wv,
+                      float *key_cache, float *value_cache, float *q_pre, float *k_pre,
+                      float *v_pre, float *q_rot, float *att_out)
+{
+    try {
+        Config c = make_config(dim, n_heads, n_kv_heads, n_layers, seq_len);
+        const size_t hd = dim / n_heads, kv_dim = (size_t)n_kv_heads * hd;
+        const size_t cache_n = (size_t)n_layers * seq_len * kv_dim;
+        Weights w;
+        auto eng = make_engine(c, wq, wk, wv, layer, w);
+        if (eng->state.key_cache.size() != cache_n) throw std::runtime_error("cache size");
+        std::memcpy(eng->state.key_cache.data(), key_cache, sizeof(float) * cache_n);
+        std::memcpy(eng->state.value_cache.data(), value_cache, sizeof(float) * cache_n);
+
+        std::vector<float> x(x_in, x_in + dim), xb(dim);
+        FloatTransformer::rmsnorm(xb.data(), x.data(), eng->weights.rms_att_weight + (size_t)layer * dim, dim);
+        FloatTransformer::matmul(q_pre, xb.data(), eng->weights.wq + (size_t)layer * dim * dim, dim, dim);
+        FloatTransformer::matmul(k_pre, xb.data(), eng->weights.wk + (size_t)layer * dim * kv_dim, dim, (int)kv_dim);
+        FloatTransformer::matmul(v_pre, xb.data(), eng->weights.wv + (size_t)layer * dim * kv_dim, dim, (int)kv_dim);
+
+        eng->run_layer(layer, pos, x.data());
+
+        std::memcpy(key_cache, eng->state.key_cache.data(), sizeof(float) * cache_n);
+        std::memcpy(value_cache, eng->state.value_cache.data(), sizeof(float) * cache_n);
+        std::memcpy(q_rot, eng->state.q.data(), sizeof(float) * dim);
+        std::memcpy(att_out, eng->state.xb2.data(), sizeof(float) * dim);
+        return 0;
+    } catch (const std::exception &e) {
+        std::cerr << "leapref_run_layer: " << e.what() << "\n";
+        return -1;
+    }
+}
+
+// clear_kv_cache (FloatTransformer.cpp:74-77) on a filled engine; returns the
+// number of nonzero floats left in either cache (0 expected).
+long leapref_clear_check(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len)
+{
+    Config c = make_config(dim, n_heads, n_kv_heads, n_layers, seq_len);
+    std::vector<float> wq((size_t)dim * dim), wk((size_t)dim * dim), wv((size_t)dim * dim);
+    Weights w;
+    auto eng = make_engine(c, wq.data(), wk.data(), wv.data(), 0, w);
+    std::fill(eng->state.key_cache.begin(), eng->state.key_cache.end(), 1.0f);
+    std::fill(eng->state.value_cache.begin(), eng->state.value_cache.end(), 2.0f);
+    eng->clear_kv_cache();
+    long nz = 0;
+    for (float f : eng->state.key_cache) nz += f != 0.0f;
+    for (float f : eng->state.value_cache) nz += f != 0.0f;
+    return nz;
+}
+
+}  // extern "C"

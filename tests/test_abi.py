@@ -1,0 +1,81 @@
+"""The C-ABI library: loads, exports what the header declares, rejects bad
+arguments with negative errno codes (host-side checks, no GPU needed)."""
+import ctypes
+import errno
+import os
+import re
+
+import pytest
+
+from leap_amd import attention as A
+from tests.conftest import gpu_available
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "leap_hip_attention.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(leap_hip_attention_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = A.load_library()
+    names = _declared()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(A.EXPORTS)
+
+
+def _create(**kw):
+    lib = A.load_library()
+    base = dict(n_layers=2, layer_begin=0, layer_end=2, n_heads=8, n_kv_heads=2, head_dim=128,
+                seq_len=64, rope_theta=500000.0, max_batch=1, device=0)
+    base.update(kw)
+    cfg = A.Config(*[base[f] for f, _ in A.Config._fields_])
+    h = ctypes.c_void_p()
+    rc = lib.leap_hip_attention_create(ctypes.byref(cfg), ctypes.byref(h))
+    msg = lib.leap_hip_attention_last_error(None).decode()
+    if rc == 0:
+        lib.leap_hip_attention_destroy(h)
+    return rc, msg
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(n_kv_heads=3), "multiple"),
+    (dict(n_heads=0), "multiple"),
+    (dict(head_dim=96), "head_dim"),
+    (dict(head_dim=128, n_heads=32, n_kv_heads=2), "head_dim"),  # 16 q heads per kv head
+    (dict(layer_begin=1, layer_end=1), "layer range"),
+    (dict(layer_end=3), "layer range"),
+    (dict(seq_len=0), "seq_len"),
+    (dict(max_batch=0), "max_batch"),
+])
+def test_create_rejects_bad_config(kw, fragment):
+    rc, msg = _create(**kw)
+    assert rc == -errno.EINVAL
+    assert fragment in msg
+
+
+def test_create_without_gpu_reports_enodev():
+    if gpu_available():
+        pytest.skip("a GPU is present")
+    rc, msg = _create()
+    assert rc == -errno.ENODEV and "device" in msg
+
+
+def test_null_arguments():
+    lib = A.load_library()
+    assert lib.leap_hip_attention_create(None, None) == -errno.EINVAL
+    assert lib.leap_hip_attention_destroy(None) == 0
+    assert lib.leap_hip_attention_step(None, 0, 0, None, None, None, None) == -errno.EINVAL
+    assert lib.leap_hip_attention_clear(None) == -errno.EINVAL
+    assert lib.leap_hip_attention_kv_upload(None, 0, 0, 0, 1, None, None) == -errno.EINVAL
+    assert lib.leap_hip_attention_set_split(None, 64) == -errno.EINVAL
+
+
+def test_python_binding_raises_leaperror():
+    with pytest.raises(A.LeapError) as ei:
+        A.HipAttention(n_heads=8, n_kv_heads=3, head_dim=128, seq_len=16)
+    assert ei.value.code == -errno.EINVAL

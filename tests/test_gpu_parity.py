@@ -1,0 +1,277 @@
+"""HIP path vs the oracle, through the C-ABI, on seeded inputs.
+
+Bar: max |delta| <= 1e-4 * max |oracle output| for the attention output
+(fp32 reductions reordered); bit-exact for the RoPE table, the rotated k and
+the v written into cache[layer][pos], and every other cache row.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from leap_amd.attention import HipAttention, LeapError
+from tests.helpers import REL_TOL, assert_close, normal, rng_for, rope_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _needs_gpu(hip_device):
+    return hip_device
+
+
+def _oracle_for(att: HipAttention, layer_rows_k, layer_rows_v, theta):
+    orc = O.Oracle(1, att.n_heads, att.n_kv_heads, att.head_dim, att.seq_len, theta=theta)
+    n = layer_rows_k.shape[0]
+    orc.key_cache[0, :n] = layer_rows_k
+    orc.value_cache[0, :n] = layer_rows_v
+    return orc
+
+
+def _step_and_check(att, seq_layer, pos, q, k, v, theta, layer_index=0, seq=0, out=None,
+                    rel=REL_TOL):
+    """Run the oracle on the device cache rows [0, pos) of (seq, layer) and
+    compare with `out` (the HIP result) and with the cache row at pos."""
+    kr, vr = att.kv_download(seq, seq_layer, 0, pos + 1)
+    orc = _oracle_for(att, kr[:pos], vr[:pos], theta)
+    want, _ = orc.step(0, pos, q, k, v)
+    err = assert_close(out, want, rel=rel)
+    assert np.array_equal(kr[pos], orc.key_cache[0, pos]), "rotated k row differs"
+    assert np.array_equal(vr[pos], orc.value_cache[0, pos]), "v row differs"
+    return err
+
+
+# ---- RoPE table --------------------------------------------------------------------
+
+@pytest.mark.parametrize("theta,hd,seq_len", [(500000.0, 128, 131072), (10000.0, 64, 256),
+                                              (500000.0, 64, 4096)])
+def test_rope_table_bitwise(theta, hd, seq_len):
+    with HipAttention(4, 4, hd, seq_len, rope_theta=theta) as att:
+        c, s = att.rope_download()
+    oc, os_ = O.rope_table(seq_len, hd, theta)
+    assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+# ---- golden fixtures from the reference ------------------------------------------
+
+def test_reference_golden_fixtures():
+    import glob
+    import os
+    gold = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    for path in sorted(glob.glob(os.path.join(gold, "run_layer_*.npz"))):
+        with np.load(path, allow_pickle=False) as z:
+            fx = {k: z[k] for k in z.files}
+        dim, nh, nkv, L, sl, layer, pos = (int(v) for v in fx["dims"])
+        hd = dim // nh
+        with HipAttention(nh, nkv, hd, sl, n_layers=L) as att:
+            if pos:
+                att.kv_upload(0, layer, 0, fx["k_rows"], fx["v_rows"])
+            out = att.step(layer, pos, fx["q_pre"], fx["k_pre"], fx["v_pre"])
+            kr, vr = att.kv_download(0, layer, pos, pos + 1)
+        assert_close(out, fx["out"], what=os.path.basename(path))
+        assert np.array_equal(kr[0], fx["k_slot"]) and np.array_equal(vr[0], fx["v_slot"])
+
+
+# ---- single sequence, many shapes, forced split-K chunkings -----------------------
+
+SHAPES = [  # n_heads, n_kv_heads, head_dim
+    (32, 4, 64), (32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 2, 128), (8, 4, 64), (4, 4, 64),
+    (16, 16, 64), (8, 2, 64),
+]
+
+
+@pytest.mark.parametrize("nh,nkv,hd", SHAPES)
+@pytest.mark.parametrize("T,split", [(1, 0), (2, 0), (64, 0), (65, 64), (300, 128), (1000, 64),
+                                     (2049, 0), (777, 256)])
+def test_step_shapes_and_splits(nh, nkv, hd, T, split):
+    theta = 10000.0 if hd == 64 else 500000.0
+    rng = rng_for(nh, nkv, hd, T, split)
+    seq_len = T + 5
+    with HipAttention(nh, nkv, hd, seq_len, n_layers=2, rope_theta=theta) as att:
+        if split:
+            att.set_split(split)
+        pos = T - 1
+        att.kv_upload(0, 1, 0, normal(rng, (pos, nkv * hd), hd), normal(rng, (pos, nkv * hd), hd))
+        q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+        out = att.step(1, pos, q, k, v)
+        _step_and_check(att, 1, pos, q, k, v, theta, out=out)
+        # the other layer is untouched
+        k0, v0 = att.kv_download(0, 0, 0, seq_len)
+        assert not k0.any() and not v0.any()
+
+
+def test_first_position_returns_v_exactly():
+    with HipAttention(32, 8, 128, 16) as att:
+        rng = rng_for(5)
+        q, k, v = normal(rng, 4096, 128), normal(rng, 1024, 128), normal(rng, 1024, 128)
+        out = att.step(0, 0, q, k, v)
+    want = np.concatenate([v.reshape(8, 128)[h // 4] for h in range(32)])
+    assert np.array_equal(out, want)
+
+
+def test_sequential_decode_matches_oracle_and_cache_bitwise():
+    nh, nkv, hd, n = 16, 4, 128, 150
+    rng = rng_for(77)
+    orc = O.Oracle(2, nh, nkv, hd, 160)
+    with HipAttention(nh, nkv, hd, 160, n_layers=2) as att:
+        att.set_split(64)
+        for pos in range(n):
+            for layer in (0, 1):
+                q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+                out = att.step(layer, pos, q, k, v)
+                want, _ = orc.step(layer, pos, q, k, v)
+                assert_close(out, want, what=f"pos {pos} layer {layer}")
+        for layer in (0, 1):
+            kr, vr = att.kv_download(0, layer, 0, 160)
+            assert np.array_equal(kr, orc.key_cache[layer]) and np.array_equal(vr, orc.value_cache[layer])
+
+
+# ---- full-size configurations -------------------------------------------------------
+
+def test_llama3_8b_ctx4096_all_layers_all_heads():
+    """32 layers, 32/8/128, T = 4096, theta 500000, seeded N(0,1)/sqrt(128)."""
+    L, nh, nkv, hd, T = 32, 32, 8, 128, 4096
+    with HipAttention(nh, nkv, hd, T, n_layers=L) as att:
+        att.kv_fill_normal(0x4C454150 + 1, 1.0 / np.sqrt(hd))
+        rng = rng_for(2, 4096)
+        worst = 0.0
+        for layer in range(L):
+            q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+            out = att.step(layer, T - 1, q, k, v)
+            worst = max(worst, _step_and_check(att, layer, T - 1, q, k, v, 500000.0, out=out))
+    print(f"llama3-8b ctx4096: worst max|delta|/Linf over 32 layers = {worst:.2e}")
+
+
+def test_tinyllama_ctx256_both_thetas():
+    nh, nkv, hd, T = 32, 4, 64, 256
+    for theta in (10000.0, 500000.0):
+        with HipAttention(nh, nkv, hd, T, rope_theta=theta) as att:
+            att.kv_fill_normal(0x4C454150 + 0, 1.0 / np.sqrt(hd))
+            rng = rng_for(1, int(theta))
+            q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+            out = att.step(0, T - 1, q, k, v)
+            _step_and_check(att, 0, T - 1, q, k, v, theta, out=out)
+
+
+def test_long_context_planted_keys():
+    """Llama-3.1-8B head config at T = 131072 with planted high-score keys in
+    the first chunk, a middle chunk, across a chunk boundary and the last
+    chunk; one held layer."""
+    nh, nkv, hd, T = 32, 8, 128, 131072
+    with HipAttention(nh, nkv, hd, T, n_layers=32, layer_begin=17, layer_end=18) as att:
+        att.kv_fill_normal(0x4C454150 + 4, 1.0 / np.sqrt(hd))
+        rng = rng_for(4, T)
+        q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+        c, s = O.rope_table(T, hd, 500000.0)
+        qr = rope_f32(q, c[T - 1], s[T - 1]).reshape(nh, hd).astype(np.float64)
+        plants = {0: (3, 300.0), 1: (65000, 420.0), 2: (98303, 520.0), 3: (98304, 500.0),
+                  5: (T - 2, 460.0), 7: (1, 350.0)}
+        for kvh, (p_pos, alpha) in plants.items():
+            h = kvh * (nh // nkv)  # first q head of the group
+            kr, _ = att.kv_download(0, 17, p_pos, p_pos + 1)
+            kr = kr.reshape(nkv, hd)
+            kr[kvh] = (qr[h] * alpha / np.dot(qr[h], qr[h])).astype(np.float32)
+            att.kv_upload(0, 17, p_pos, kr.reshape(1, -1), None)
+        out = att.step(17, T - 1, q, k, v)
+        _step_and_check(att, 17, T - 1, q, k, v, 500000.0, out=out)
+
+
+def test_batched_ragged_llama3_8b():
+    """64 sequences, one layer, T_i ~ U[512, 8192] (the batched config's shape)."""
+    nh, nkv, hd, S, T_max = 32, 8, 128, 64, 8192
+    rng = rng_for(3, S)
+    Ts = rng.integers(512, T_max + 1, size=S)
+    with HipAttention(nh, nkv, hd, T_max, n_layers=32, layer_begin=5, layer_end=6,
+                      max_batch=S) as att:
+        att.kv_fill_normal(0x4C454150 + 2, 1.0 / np.sqrt(hd))
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(5, Ts - 1, q, k, v)
+        for i in range(S):
+            _step_and_check(att, 5, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+def test_batched_small_ragged_with_tiny_contexts():
+    nh, nkv, hd, S = 16, 2, 128, 9
+    Ts = np.array([1, 2, 63, 64, 65, 128, 129, 700, 1500])
+    rng = rng_for(33)
+    with HipAttention(nh, nkv, hd, 1600, max_batch=12) as att:
+        att.kv_fill_normal(99, 0.1)
+        att.set_split(64)
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(0, Ts - 1, q, k, v)
+        for i in range(S):
+            _step_and_check(att, 0, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+def test_llama3_70b_stage_batch16_ctx8192():
+    """64/8/128, batch 16, T = 8192, one of the stage's 20 layers."""
+    nh, nkv, hd, S, T = 64, 8, 128, 16, 8192
+    rng = rng_for(5, S)
+    with HipAttention(nh, nkv, hd, T, n_layers=80, layer_begin=20, layer_end=21,
+                      max_batch=S) as att:
+        att.kv_fill_normal(0x4C454150 + 3, 1.0 / np.sqrt(hd))
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(20, np.full(S, T - 1), q, k, v)
+        for i in (0, 7, 15):
+            _step_and_check(att, 20, T - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+# ---- cache management and errors ----------------------------------------------------
+
+def test_clear_upload_download_roundtrip():
+    with HipAttention(8, 2, 64, 100, n_layers=3, max_batch=2) as att:
+        rng = rng_for(9)
+        k, v = normal(rng, (100, 128), 64), normal(rng, (100, 128), 64)
+        att.kv_upload(1, 2, 0, k, v)
+        kr, vr = att.kv_download(1, 2, 0, 100)
+        assert np.array_equal(kr, k) and np.array_equal(vr, v)
+        kr, _ = att.kv_download(1, 2, 10, 20)
+        assert np.array_equal(kr, k[10:20])
+        att.clear()
+        kr, vr = att.kv_download(1, 2, 0, 100)
+        assert not kr.any() and not vr.any()
+
+
+def test_step_argument_errors():
+    with HipAttention(8, 2, 64, 100, n_layers=4, layer_begin=1, layer_end=3) as att:
+        z = np.zeros(8 * 64, np.float32)
+        zk = np.zeros(2 * 64, np.float32)
+        for layer, pos in ((0, 0), (3, 0), (1, 100), (1, -1)):
+            with pytest.raises(LeapError):
+                att.step(layer, pos, z, zk, zk)
+        with pytest.raises(LeapError):
+            att.step_batched(1, [5, 200], np.zeros((2, 512), np.float32),
+                             np.zeros((2, 128), np.float32), np.zeros((2, 128), np.float32))
+        with pytest.raises(LeapError):
+            att.set_split(100)
+
+
+def test_async_entry_points_on_a_torch_stream():
+    import torch
+    nh, nkv, hd, T = 32, 8, 128, 3000
+    rng = rng_for(12)
+    q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+    with HipAttention(nh, nkv, hd, T, max_batch=2) as att:
+        att.kv_fill_normal(5, 0.1)
+        ref = att.step(0, T - 1, q, k, v)
+        dq, dk, dv = (torch.from_numpy(a).cuda() for a in (q, k, v))
+        dout = torch.empty(nh * hd, device="cuda")
+        s = torch.cuda.Stream()
+        att.step_async(0, T - 1, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dout.data_ptr(),
+                       s.cuda_stream)
+        s.synchronize()
+        assert np.array_equal(dout.cpu().numpy(), ref)
+        # batched async with device positions
+        pos = torch.tensor([T - 1, 17], dtype=torch.int32, device="cuda")
+        bq, bk, bv = (torch.stack([t, t]) for t in (dq, dk, dv))
+        bout = torch.empty(2, nh * hd, device="cuda")
+        att.step_batched_async(0, 2, pos.data_ptr(), T - 1, bq.data_ptr(), bk.data_ptr(),
+                               bv.data_ptr(), bout.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert np.array_equal(bout[0].cpu().numpy(), ref)
+        _step_and_check(att, 0, 17, q, k, v, 500000.0, seq=1, out=bout[1].cpu().numpy())

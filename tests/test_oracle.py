@@ -1,0 +1,254 @@
+"""Pins for the oracle (CPU restatement of the reference's attention block).
+
+Each check is chosen so that a plausible slip fails it: the reference's own
+outputs (golden fixtures written by tests/golden/make_golden.py from
+oracle/_ref, and the live reference driver when it is built), a float64
+textbook attention on tiny shapes, closed forms, and deliberately wrong
+variants of the oracle that must fail those pins.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.helpers import assert_close, attention_f64, normal, rel_err, rng_for, rope_f32
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not os.path.isfile(O.ORACLE_SO):
+        O.build(ref=False)
+
+
+def _load(path):
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _run_fixture(fx, mutant=0):
+    dim, nh, nkv, L, sl, layer, pos = (int(v) for v in fx["dims"])
+    hd = dim // nh
+    orc = O.Oracle(L, nh, nkv, hd, sl)
+    orc.key_cache[layer, :pos] = fx["k_rows"]
+    orc.value_cache[layer, :pos] = fx["v_rows"]
+    out, q_rot = orc.step(layer, pos, fx["q_pre"], fx["k_pre"], fx["v_pre"], mutant=mutant)
+    return out, q_rot, orc.key_cache[layer, pos], orc.value_cache[layer, pos]
+
+
+# ---- RoPE table (FloatTransformer.cpp:56-72) ---------------------------------
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "rope_*.npz"))))
+def test_rope_table_bitwise_reference_golden(path):
+    fx = _load(path)
+    dim, nh, sl = (int(v) for v in fx["dims"])
+    c, s = O.rope_table(sl, dim // nh, 500000.0)
+    rows = fx["rows"]
+    assert np.array_equal(c[rows], fx["cos"])
+    assert np.array_equal(s[rows], fx["sin"])
+
+
+def test_rope_table_closed_forms():
+    for theta in (500000.0, 10000.0):
+        c, s = O.rope_table(4096, 128, theta)
+        assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)  # pos 0: identity
+        # freq_0 = 1: column 0 is cos/sin of the integer position itself.
+        pos = np.arange(4096)
+        assert np.abs(c[:, 0] - np.cos(pos)).max() < 2e-6
+        assert np.abs(s[:, 0] - np.sin(pos)).max() < 2e-6
+        assert np.abs(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2 - 1).max() < 1e-6
+        # column i follows theta^(-2i/hd) (float64 textbook, fp32-angle tolerance)
+        i = np.arange(64)
+        ang = 1000.0 * theta ** (-(2.0 * i) / 128.0)
+        assert np.abs(c[1000] - np.cos(ang)).max() < 1e-3
+        assert np.abs(s[1000] - np.sin(ang)).max() < 1e-3
+    # different theta -> different table (the parameter is used)
+    assert not np.array_equal(O.rope_table(64, 64, 10000.0)[0], O.rope_table(64, 64, 500000.0)[0])
+
+
+def test_rope_table_bitwise_live_reference():
+    if not O.ref_available():
+        pytest.skip("reference driver not built (reference sources absent)")
+    for dim, nh, sl in [(2048, 32, 300), (4096, 32, 5000), (1024, 4, 64)]:
+        rc, rs = O.ref_rope_table(dim, nh, sl)
+        oc, os_ = O.rope_table(sl, dim // nh, 500000.0)
+        assert np.array_equal(rc, oc) and np.array_equal(rs, os_)
+
+
+# ---- the attention step against the reference ----------------------------------
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "run_layer_*.npz"))))
+def test_step_reference_golden(path):
+    fx = _load(path)
+    out, q_rot, k_slot, v_slot = _run_fixture(fx)
+    assert np.array_equal(q_rot, fx["q_rot"]), "rotated q differs from the reference"
+    assert np.array_equal(k_slot, fx["k_slot"]), "rotated k in the cache differs"
+    assert np.array_equal(v_slot, fx["v_slot"]), "v in the cache differs"
+    # observed 0 .. 3e-7: softmax reductions vectorised differently under -ffast-math
+    assert_close(out, fx["out"], rel=2e-6)
+
+
+@pytest.mark.parametrize("dim,nh,nkv,L,sl,layer,pos", [
+    (512, 8, 2, 3, 100, 2, 99),
+    (1024, 16, 16, 1, 37, 0, 36),
+    (2048, 16, 2, 2, 20, 0, 7),
+])
+def test_step_live_reference(dim, nh, nkv, L, sl, layer, pos):
+    if not O.ref_available():
+        pytest.skip("reference driver not built (reference sources absent)")
+    rng = rng_for(dim, pos, 11)
+    hd, kvd = dim // nh, nkv * (dim // nh)
+    x = rng.standard_normal(dim).astype(np.float32)
+    wq = normal(rng, (dim, dim), dim)
+    wk = normal(rng, (kvd, dim), dim)
+    wv = normal(rng, (kvd, dim), dim)
+    kc = normal(rng, (L, sl, kvd), hd)
+    vc = normal(rng, (L, sl, kvd), hd)
+    r = O.ref_run_layer(dim, nh, nkv, L, sl, layer, pos, x, wq, wk, wv, kc, vc)
+    orc = O.Oracle(L, nh, nkv, hd, sl)
+    orc.key_cache[:] = kc
+    orc.value_cache[:] = vc
+    out, q_rot = orc.step(layer, pos, r["q_pre"], r["k_pre"], r["v_pre"])
+    assert np.array_equal(q_rot, r["q_rot"])
+    assert np.array_equal(orc.key_cache, r["key_cache"])
+    assert np.array_equal(orc.value_cache, r["value_cache"])
+    assert_close(out, r["out"], rel=2e-6)
+
+
+def test_clear_matches_reference():
+    orc = O.Oracle(2, 4, 2, 8, 16)
+    orc.key_cache[:] = 1
+    orc.value_cache[:] = 2
+    orc.clear()
+    assert not orc.key_cache.any() and not orc.value_cache.any()
+    if O.ref_available():
+        assert O.ref().leapref_clear_check(32, 4, 2, 2, 16) == 0
+
+
+# ---- independent pins: float64 brute force and closed forms --------------------
+
+def _tiny(seed, nh=4, nkv=2, hd=8, T=64, theta=10000.0, sl=80):
+    rng = rng_for(seed, nh, nkv, hd, T)
+    orc = O.Oracle(1, nh, nkv, hd, sl, theta=theta)
+    pos = T - 1
+    orc.key_cache[0, :pos] = normal(rng, (pos, nkv * hd), hd)
+    orc.value_cache[0, :pos] = normal(rng, (pos, nkv * hd), hd)
+    q = normal(rng, nh * hd, hd)
+    k = normal(rng, nkv * hd, hd)
+    v = normal(rng, nkv * hd, hd)
+    return orc, pos, q, k, v
+
+
+def _bruteforce(orc, pos, q, k, v):
+    c, s = orc.cos[pos], orc.sin[pos]
+    K = orc.key_cache[0, :pos + 1].copy()
+    V = orc.value_cache[0, :pos + 1].copy()
+    K[pos] = rope_f32(k, c, s)
+    V[pos] = v
+    return attention_f64(rope_f32(q, c, s), K, V, orc.n_heads, orc.n_kv_heads, orc.head_dim)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,T", [(4, 2, 8, 64), (4, 4, 8, 1), (8, 2, 16, 33),
+                                         (6, 3, 10, 17), (4, 1, 64, 50)])
+def test_step_float64_bruteforce(nh, nkv, hd, T):
+    orc, pos, q, k, v = _tiny(1, nh, nkv, hd, T)
+    want = _bruteforce(orc, pos, q, k, v)
+    out, _ = orc.step(0, pos, q, k, v)
+    assert_close(out, want, rel=1e-5)
+
+
+def test_first_position_returns_v():
+    orc, _, q, k, v = _tiny(2, T=1)
+    out, _ = orc.step(0, 0, q, k, v)
+    kv_mul = orc.n_heads // orc.n_kv_heads
+    want = np.concatenate([v.reshape(orc.n_kv_heads, -1)[h // kv_mul] for h in range(orc.n_heads)])
+    assert np.array_equal(out, want)
+    assert np.array_equal(orc.key_cache[0, 0], k)  # pos 0 rotation is the identity
+
+
+def test_identical_keys_give_mean_of_values():
+    orc, pos, q, k, v = _tiny(3, T=40)
+    c, s = orc.cos[pos], orc.sin[pos]
+    krot = rope_f32(k, c, s)
+    orc.key_cache[0, :pos] = krot  # every row equals the new (rotated) key
+    out, _ = orc.step(0, pos, q, k, v)
+    V = orc.value_cache[0, :pos + 1].astype(np.float64).reshape(pos + 1, orc.n_kv_heads, -1)
+    kv_mul = orc.n_heads // orc.n_kv_heads
+    want = np.concatenate([V[:, h // kv_mul].mean(0) for h in range(orc.n_heads)])
+    assert_close(out, want, rel=1e-5)
+
+
+def test_dominant_key_returns_its_value():
+    orc, pos, q, k, v = _tiny(4, nh=2, nkv=1, hd=8, T=30)
+    c, s = orc.cos[pos], orc.sin[pos]
+    qr = rope_f32(q, c, s).reshape(2, 8)
+    planted = 7
+    orc.key_cache[0, planted] = (qr[0] / np.linalg.norm(qr[0]) * 400.0).astype(np.float32)
+    out, _ = orc.step(0, pos, q, k, v)
+    # head 0 sees a score gap of ~400*|q|/sqrt(8) >> 104: every other weight underflows
+    assert np.array_equal(out[:8], orc.value_cache[0, planted])
+
+
+def test_permuting_positions_leaves_output_unchanged():
+    orc, pos, q, k, v = _tiny(5, T=48)
+    out1, _ = orc.step(0, pos, q, k, v)
+    perm = rng_for(5, 99).permutation(pos)
+    orc2, _, _, _, _ = _tiny(5, T=48)
+    orc2.key_cache[0, :pos] = orc2.key_cache[0, perm]
+    orc2.value_cache[0, :pos] = orc2.value_cache[0, perm]
+    out2, _ = orc2.step(0, pos, q, k, v)
+    assert_close(out2, out1, rel=1e-6)
+
+
+def test_gqa_heads_with_equal_q_agree():
+    orc, pos, q, k, v = _tiny(6, nh=8, nkv=2, hd=8, T=20)
+    qh = q.reshape(8, 8)
+    qh[1:4] = qh[0]  # heads 0..3 share KV head 0
+    out, _ = orc.step(0, pos, qh.reshape(-1), k, v)
+    o = out.reshape(8, 8)
+    for h in (1, 2, 3):
+        assert np.array_equal(o[h], o[0])
+
+
+def test_relative_position_property():
+    # score(q at m, k at n) depends on m - n only (rotation group), up to table rounding
+    hd = 16
+    orc = O.Oracle(1, 1, 1, hd, 64, theta=10000.0)
+    rng = rng_for(7)
+    q, k = normal(rng, hd, hd), normal(rng, hd, hd)
+
+    def score(m, n):
+        return float(np.dot(rope_f32(q, orc.cos[m], orc.sin[m]).astype(np.float64),
+                            rope_f32(k, orc.cos[n], orc.sin[n]).astype(np.float64)))
+    for d in (0, 3, 11):
+        ref = score(d, 0)
+        for m in (d + 5, d + 20, 60):
+            assert abs(score(m, m - d) - ref) < 1e-5
+
+
+# ---- the pins catch plausible mistakes -------------------------------------------
+
+@pytest.mark.parametrize("mutant", [1, 2, 3])
+def test_mutants_fail_the_pins(mutant):
+    failed = []
+    for path in sorted(glob.glob(os.path.join(GOLDEN, "run_layer_*.npz"))):
+        fx = _load(path)
+        out, q_rot, k_slot, _ = _run_fixture(fx, mutant=mutant)
+        failed.append(rel_err(out, fx["out"]) > 1e-4 or not np.array_equal(k_slot, fx["k_slot"]))
+    orc, pos, q, k, v = _tiny(8, nh=8, nkv=2, hd=8, T=40)
+    want = _bruteforce(orc, pos, q, k, v)
+    out, _ = orc.step(0, pos, q, k, v, mutant=mutant)
+    failed.append(rel_err(out, want) > 1e-5)
+    assert any(failed), f"mutant {mutant} passed every pin"
+
+
+def test_rejects_bad_arguments():
+    orc = O.Oracle(1, 4, 3, 8, 16)  # 4 % 3 != 0
+    with pytest.raises(ValueError):
+        orc.step(0, 0, np.zeros(32, np.float32), np.zeros(24, np.float32), np.zeros(24, np.float32))
+    orc = O.Oracle(1, 4, 2, 8, 16)
+    with pytest.raises(ValueError):
+        orc.step(0, 16, np.zeros(32, np.float32), np.zeros(16, np.float32), np.zeros(16, np.float32))
