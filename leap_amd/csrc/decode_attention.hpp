@@ -2,18 +2,30 @@
 //
 // One launch performs the whole attention block of one layer step for one or
 // more sequences (the reference's FloatTransformer.cpp:396-662):
-//   - RoPE of q (every workgroup rotates the q heads of its KV group from the
-//     fp32 table row `pos`, FloatTransformer.cpp:404-494),
+//   - RoPE of q: every workgroup rotates the q heads of its KV group with the
+//     fp32 table row `pos` (FloatTransformer.cpp:404-494);
 //   - the KV append: the workgroup whose chunk holds `pos` rotates k_new,
-//     stores k_new/v_new into cache[layer][pos] and uses them in registers,
-//   - split-K flash decoding over the KV positions [0, pos]: each workgroup
-//     owns one (sequence, KV head, chunk of positions), streams its K and V
-//     rows straight into registers with 128-bit loads and serves all q heads
-//     of the KV group from those registers (GQA score, :496-630), with an
-//     online softmax (running max/sum, :216-238) and the weighted-V
-//     accumulation (:634-661),
-//   - the merge of the chunk partials, done by the last workgroup of each
-//     (sequence, KV head) to finish (an atomic arrival counter it resets).
+//     stores k_new / v_new into cache[layer][pos] and uses them in registers;
+//   - split-K flash decoding over the positions [0, pos]: a workgroup owns one
+//     (sequence, KV head, chunk of positions); its eight waves stream
+//     interleaved sub-tiles of K and V rows straight into registers with
+//     128-bit buffer loads, and every wave serves all q heads of the KV group
+//     from those registers: GQA score (:496-630), online softmax (running
+//     max / sum, :216-238) and the weighted-V accumulation (:634-661);
+//   - the merge of the chunk partials: each chunk writes an unnormalised
+//     partial (o, max, sum) to the workspace and counts itself in with an
+//     atomic; the last chunk of a (sequence, KV head) to arrive combines all
+//     partials and resets the counter.
+//
+// XCD placement.  Workgroups are dealt to the XCDs round-robin by workgroup
+// id, so id % 8 names the XCD (the same holds within a 1-, 2- or 4-XCD
+// partition).  The grid is numbered so that every workgroup of one
+// (sequence, KV head) group has id % 8 == group % 8: the whole group runs on
+// one XCD and shares that XCD's L2.  Partials, the arrival counter and the
+// merge reads therefore stay in L2 (stores drain to L2, the atomic executes in
+// L2, merge loads bypass only L1) instead of travelling to memory.  Within a
+// group, consecutive chunks are neighbouring ids, and with eight KV heads a
+// row's eight head slices are requested by neighbouring workgroups.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,12 +34,13 @@
 namespace leap {
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;                 // waves per workgroup
-constexpr int kThreads = kWave * kWaves;  // 256
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
-// Positions one workgroup pass covers (kWaves sub-tiles of 2048/HD rows);
-// chunk sizes are multiples of it.
-__host__ __device__ constexpr int rows_per_pass(int hd) { return kWaves * (2048 / hd); }
+constexpr int kXcds = 8;                  // XCDs of an MI355X
+constexpr int kSc0 = 1;                   // cache policy: bypass L1, read L2
+
+// Positions one workgroup pass covers with NW waves (NW sub-tiles of 2048/HD
+// rows); chunk sizes are multiples of it.
+__host__ __device__ constexpr int rows_per_pass(int hd, int nw) { return nw * (2048 / hd); }
 
 struct StepArgs {
     const float *q;      // [n_seq][n_heads*HD], pre-RoPE
@@ -47,40 +60,139 @@ struct StepArgs {
     int seq_len;
     int n_heads;
     int n_kv_heads;
-    int chunk;           // positions per workgroup, multiple of rows_per_pass(HD)
+    int chunk;           // positions per workgroup, multiple of rows_per_pass(HD, NW)
+    int grid_chunks;     // chunks per sequence in the launch grid
+    int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
 };
 
+// ---- buffer access ------------------------------------------------------------
+//
+// Raw buffer loads take 32-bit byte offsets from a base and return zero past
+// num_records bytes, which masks rows beyond the valid range without
+// branches.
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+constexpr int kRsrcWord3 = 0x00020000;  // raw 32-bit dword access, gfx9 family
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, kRsrcWord3);
+}
+
+// The loaded vector is reinterpreted whole (f32x4), never lane by lane: the
+// compiler narrows a b128 buffer load to one dword when its lanes are
+// bit-cast one at a time.
+template <int AUX = 0>
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+template <int AUX = 0>
+__device__ __forceinline__ float2 buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    const f32x2 v = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX));
+    return make_float2(v.x, v.y);
+}
+
+template <int AUX = 0>
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 x)
+{
+    const f32x4 v = {x.x, x.y, x.z, x.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)off, 0, AUX);
+}
+
+template <int AUX = 0>
+__device__ __forceinline__ void buf_store2(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 x)
+{
+    const f32x2 v = {x.x, x.y};
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, (int)off, 0, AUX);
+}
+
 // ---- wave helpers ---------------------------------------------------------
+//
+// Cross-lane reductions use DPP (fused into the VALU op) inside 16-lane rows:
+// quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes differing in bit 0 and
+// bit 1; once values agree inside each quad (or 8-lane half row),
+// row_half_mirror (or row_mirror) brings in the other quad (or half row).
+// Across rows, the four row leaders are read with v_readlane, which leaves a
+// wave-uniform result.
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL,
+                                                              0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+
+// Sum over the aligned group of W lanes (W = 1..16), result in every lane.
 template <int W>
-__device__ __forceinline__ float xor_sum(float x)
+__device__ __forceinline__ float group_sum(float x)
 {
-#pragma unroll
-    for (int o = 1; o < W; o <<= 1) x += __shfl_xor(x, o, kWave);
+    if constexpr (W >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+    if constexpr (W >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+    if constexpr (W >= 8) x += dpp<0x141>(x);  // row_half_mirror
+    if constexpr (W >= 16) x += dpp<0x140>(x); // row_mirror
+    static_assert(W <= 16, "group_sum covers one row");
     return x;
 }
 
-// max over lanes that differ only in bits [log2(FROM), 6)
+// Max / sum over the wave of values that are uniform inside each aligned
+// group of FROM lanes (FROM = 1, 2, 4, 8 or 16); the result is wave-uniform.
 template <int FROM>
-__device__ __forceinline__ float xor_max_above(float x)
+__device__ __forceinline__ float groups_max(float x)
 {
-#pragma unroll
-    for (int o = FROM; o < kWave; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, kWave));
-    return x;
+    if constexpr (FROM < 16) {
+        if constexpr (FROM <= 1) x = fmaxf(x, dpp<0xB1>(x));
+        if constexpr (FROM <= 2) x = fmaxf(x, dpp<0x4E>(x));
+        if constexpr (FROM <= 4) x = fmaxf(x, dpp<0x141>(x));
+        x = fmaxf(x, dpp<0x140>(x));
+    }
+    return fmaxf(fmaxf(lane_value(x, 0), lane_value(x, 16)),
+                 fmaxf(lane_value(x, 32), lane_value(x, 48)));
 }
 
 template <int FROM>
-__device__ __forceinline__ float xor_sum_above(float x)
+__device__ __forceinline__ float groups_sum(float x)
 {
-#pragma unroll
-    for (int o = FROM; o < kWave; o <<= 1) x += __shfl_xor(x, o, kWave);
-    return x;
+    if constexpr (FROM < 16) {
+        if constexpr (FROM <= 1) x += dpp<0xB1>(x);
+        if constexpr (FROM <= 2) x += dpp<0x4E>(x);
+        if constexpr (FROM <= 4) x += dpp<0x141>(x);
+        x += dpp<0x140>(x);
+    }
+    return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
 }
 
 __device__ __forceinline__ float dot4(float4 a, float4 b)
 {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+__device__ __forceinline__ void fma4(float4 &acc, float p, float4 v)
+{
+    acc.x += p * v.x;
+    acc.y += p * v.y;
+    acc.z += p * v.z;
+    acc.w += p * v.w;
+}
+
+__device__ __forceinline__ void scale4(float4 &acc, float s)
+{
+    acc.x *= s;
+    acc.y *= s;
+    acc.z *= s;
+    acc.w *= s;
 }
 
 // Interleaved-pair rotation of one float4 (two pairs) with table entry
@@ -101,8 +213,24 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 // ---- the fused decode-attention kernel --------------------------------------
 
-template <int HD, int G>
+// Rotation for q: fused multiply-adds are fine here (q is not stored).
+__device__ __forceinline__ float4 rope4_fma(float4 x, float4 t)
+{
+    float4 r;
+    r.x = x.x * t.x - x.y * t.y;
+    r.y = x.y * t.x + x.x * t.y;
+    r.z = x.z * t.z - x.w * t.w;
+    r.w = x.w * t.z + x.z * t.w;
+    return r;
+}
+
+// Growth of the running max (log2 units) tolerated before the accumulators
+// are rescaled: p = 2^(s - m_ref) stays below 2^kLazyMax.
+constexpr float kLazyMax = 8.0f;
+
+template <int HD, int G, int NW>
 struct Shape {
+    static constexpr int THREADS = NW * kWave;
     static constexpr int LPR = (HD * G >= 1024) ? 16 : 8;  // lanes per K row
     static constexpr int NF = HD / (4 * LPR);              // float4 per lane per K row
     static constexpr int RPK = kWave / LPR;                // K rows per load set
@@ -111,23 +239,30 @@ struct Shape {
     static constexpr int LPV = HD / 4;                     // lanes per V row
     static constexpr int RPV = kWave / LPV;                // V rows per load set
     static constexpr int VS = R / RPV;                     // V load sets per sub-tile
-    static constexpr int ROWS = kWaves * R;                // positions per workgroup pass
+    static constexpr int ROWS = NW * R;                    // positions per workgroup pass
+    static constexpr int D4 = HD / 4;                      // float4 per head row
+    static constexpr int MG = THREADS / (G * D4);          // merge: chunk lanes per head
     static_assert(HD % (4 * LPR) == 0, "head_dim vs lanes per row");
     static_assert(R % RPK == 0 && R % RPV == 0, "sub-tile shape");
     static_assert(G <= LPR, "group size vs lanes per row");
-    static_assert(ROWS == rows_per_pass(HD), "pass shape");
+    static_assert(MG >= 1 && THREADS % (G * D4) == 0, "merge layout");
 };
 
-template <int HD, int G>
-__global__ __launch_bounds__(kThreads) void decode_attention_kernel(StepArgs a)
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
 {
-    using S = Shape<HD, G>;
+    using S = Shape<HD, G, NW>;
     constexpr int LPR = S::LPR, NF = S::NF, RPK = S::RPK, R = S::R, KS = S::KS;
-    constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS;
+    constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, MG = S::MG;
 
-    const int chunk_id = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int seq = blockIdx.z;
+    // id = ((group / 8) * grid_chunks + chunk) * 8 + group % 8
+    const int xcd = blockIdx.x % kXcds;
+    const int local = blockIdx.x / kXcds;
+    const int chunk_id = local % a.grid_chunks;
+    const int group = (local / a.grid_chunks) * kXcds + xcd;
+    if (group >= a.n_groups) return;
+    const int seq = group / a.n_kv_heads;
+    const int kvh = group % a.n_kv_heads;
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
@@ -140,16 +275,22 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(StepArgs a)
 
     const int kv_dim = a.n_kv_heads * HD;
     const int q_dim = a.n_heads * HD;
+    const uint32_t row_bytes = (uint32_t)kv_dim * 4u;
     const size_t slab = (size_t)seq * (size_t)a.seq_stride;
-    const float *kc = a.k_cache + slab + (size_t)kvh * HD;
-    const float *vc = a.v_cache + slab + (size_t)kvh * HD;
+    float *kc = a.k_cache + slab + (size_t)kvh * HD;
+    float *vc = a.v_cache + slab + (size_t)kvh * HD;
+    // Rows [0, pos) of this KV head are in range; row pos and beyond read 0.
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc, (uint32_t)pos * row_bytes);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)pos * row_bytes);
+    const float *k_row_new = a.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
+    const float *v_row_new = a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
     const float *qg = a.q + (size_t)seq * q_dim + (size_t)kvh * G * HD;
     const float4 *rope_row = a.rope + (size_t)pos * (HD / 4);
 
-    __shared__ float p_lds[kWaves][R * G];
-    __shared__ float comb_o[kWaves][G][HD];
-    __shared__ float comb_ml[kWaves][G][2];
-    __shared__ float merge_w[kWaves][kMaxChunks];
+    __shared__ float p_lds[NW][R * G];
+    __shared__ float4 comb_o[NW][RPV][G][D4];
+    __shared__ float comb_l[NW][G];
+    __shared__ float comb_m[NW][G];
     __shared__ int s_last;
 
     // K layout: lane = kg*LPR + kj; lane holds dims 4*(f*LPR + kj) .. +3.
@@ -157,81 +298,94 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(StepArgs a)
     // V layout: lane = vg*LPV + vj; lane holds dims 4*vj .. +3.
     const int vg = lane / LPV, vj = lane % LPV;
 
-    // Rotated q for the G heads of this KV group, in the K layout.
-    float4 qr[G][NF];
+    // Issue order: q, table row and the new token's k / v first, then the
+    // first K/V tile, so that rotating q waits only for the small loads.
+    float4 qr[G][NF], tab[NF], knew[NF];
 #pragma unroll
     for (int f = 0; f < NF; f++) {
         const int d4 = f * LPR + kj;
-        const float4 tab = rope_row[d4];
+        tab[f] = rope_row[d4];
+        knew[f] = *reinterpret_cast<const float4 *>(k_row_new + 4 * d4);
 #pragma unroll
-        for (int h = 0; h < G; h++) {
-            const float4 x = *reinterpret_cast<const float4 *>(qg + (size_t)h * HD + 4 * d4);
-            qr[h][f] = rope4(x, tab);
-        }
+        for (int h = 0; h < G; h++)
+            qr[h][f] = *reinterpret_cast<const float4 *>(qg + (size_t)h * HD + 4 * d4);
     }
+    const float4 vnew = *reinterpret_cast<const float4 *>(v_row_new + 4 * vj);
 
     const int chunk_begin = chunk_id * a.chunk;
     const int n_sub = a.chunk / S::ROWS;
 
-    float m_run[G], l_run[G];
-    float4 acc[G];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        m_run[h] = -INFINITY;
-        l_run[h] = 0.0f;
-        acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
     float4 kb[KS][NF], vb[VS];
-
-    auto load_tile = [&](int sub, float4 (&kd)[KS][NF], float4 (&vd)[VS]) {
-        const int base = chunk_begin + (sub * kWaves + wave) * R;
+    auto load_tile = [&](int sub) {
+        const int base = chunk_begin + (sub * NW + wave) * R;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const int t = base + ks * RPK + kg;
-            const float *row = (t == pos) ? a.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD
-                                          : kc + (size_t)t * kv_dim;
+            const uint32_t roff = (uint32_t)(base + ks * RPK + kg) * row_bytes;
 #pragma unroll
-            for (int f = 0; f < NF; f++) {
-                const int d4 = f * LPR + kj;
-                kd[ks][f] = (t <= pos) ? *reinterpret_cast<const float4 *>(row + 4 * d4)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            for (int f = 0; f < NF; f++)
+                kb[ks][f] = buf_load4(k_rsrc, roff + 16u * (uint32_t)(f * LPR + kj));
         }
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
-            const int t = base + vs * RPV + vg;
-            const float *row = (t == pos) ? a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD
-                                          : vc + (size_t)t * kv_dim;
-            vd[vs] = (t <= pos) ? *reinterpret_cast<const float4 *>(row + 4 * vj)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+            const uint32_t roff = (uint32_t)(base + vs * RPV + vg) * row_bytes;
+            vb[vs] = buf_load4(v_rsrc, roff + 16u * (uint32_t)vj);
         }
     };
 
+    load_tile(0);
+
+    // k exactly as the reference rotates it (it is stored); q with the
+    // score scale folded in, so scores come out in log2 units.
+#pragma unroll
+    for (int f = 0; f < NF; f++) {
+        knew[f] = rope4(knew[f], tab[f]);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            qr[h][f] = rope4_fma(qr[h][f], tab[f]);
+            scale4(qr[h][f], a.scale_log2);
+        }
+    }
+
+    // P.V accumulators, MFMA 4x4x1 (16 blocks) layout: block b = lane / 4
+    // covers the lanes of one V row; acc[q][e][i] is head 4q+i at dim
+    // 4*vj + e of the rows this lane's half (or quarter) of the wave sees.
+    constexpr int GQ = (G + 3) / 4;
+    float m_ref[G], l_run[G];
+    f32x4 acc[GQ][4];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m_ref[h] = -INFINITY;
+        l_run[h] = 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < GQ; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[q][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
     for (int sub = 0; sub < n_sub; sub++) {
-        load_tile(sub, kb, vb);
+        if (sub > 0) load_tile(sub);
+        const int base = chunk_begin + (sub * NW + wave) * R;
 
-        const int base = chunk_begin + (sub * kWaves + wave) * R;
-
-        // The new token's row: rotate k, and append k and v to the cache.
+        // The new token's row: the rotated k_new / v_new replace the (zero)
+        // loads, and are appended to cache[layer][pos].
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const int t = base + ks * RPK + kg;
             if (t == pos) {
 #pragma unroll
                 for (int f = 0; f < NF; f++) {
-                    const int d4 = f * LPR + kj;
-                    kb[ks][f] = rope4(kb[ks][f], rope_row[d4]);
-                    *reinterpret_cast<float4 *>(const_cast<float *>(kc) + (size_t)t * kv_dim + 4 * d4) =
-                        kb[ks][f];
+                    kb[ks][f] = knew[f];
+                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (f * LPR + kj)) = knew[f];
                 }
             }
         }
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const int t = base + vs * RPV + vg;
-            if (t == pos)
-                *reinterpret_cast<float4 *>(const_cast<float *>(vc) + (size_t)t * kv_dim + 4 * vj) = vb[vs];
+            if (t == pos) {
+                vb[vs] = vnew;
+                *reinterpret_cast<float4 *>(vc + (size_t)t * kv_dim + 4 * vj) = vnew;
+            }
         }
 
         // Scores (log2 units) for the KS rows this lane group holds.
@@ -244,26 +398,43 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(StepArgs a)
                 float d = 0.f;
 #pragma unroll
                 for (int f = 0; f < NF; f++) d += dot4(qr[h][f], kb[ks][f]);
-                d = xor_sum<LPR>(d) * a.scale_log2;
+                d = group_sum<LPR>(d);
                 s[ks][h] = (t <= pos) ? d : -INFINITY;
             }
         }
 
-        // Online softmax update, per head, wave-wide.
-        float alpha[G];
+        // Online softmax with a lazily raised reference max: only when some
+        // score exceeds m_ref + kLazyMax is the wave max taken and the
+        // accumulators rescaled (always on the first valid tile).
+        float mt[G];
+        bool grow = false;
 #pragma unroll
         for (int h = 0; h < G; h++) {
-            float mt = s[0][h];
+            mt[h] = s[0][h];
 #pragma unroll
-            for (int ks = 1; ks < KS; ks++) mt = fmaxf(mt, s[ks][h]);
-            mt = xor_max_above<LPR>(mt);
-            const float m_new = fmaxf(m_run[h], mt);
-            // m_new == -inf only while every row seen so far is masked.
-            alpha[h] = (m_new == -INFINITY) ? 1.0f : fast_exp2(m_run[h] - m_new);
+            for (int ks = 1; ks < KS; ks++) mt[h] = fmaxf(mt[h], s[ks][h]);
+            grow |= mt[h] > m_ref[h] + kLazyMax;
+        }
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                s[ks][h] = (s[ks][h] == -INFINITY) ? 0.0f : fast_exp2(s[ks][h] - m_new);
-            m_run[h] = m_new;
+            for (int h = 0; h < G; h++) {
+                const float m_new = fmaxf(m_ref[h], groups_max<LPR>(mt[h]));
+                const float alpha = (m_ref[h] == -INFINITY) ? 0.0f : fast_exp2(m_ref[h] - m_new);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[h / 4][e][h % 4] *= alpha;
+                l_run[h] *= alpha;
+                m_ref[h] = m_new;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                s[ks][h] = (s[ks][h] == -INFINITY) ? 0.0f : fast_exp2(s[ks][h] - m_ref[h]);
+                // every lane of a K row group holds the same p: l is kept per
+                // group here and summed across the groups once at the end
+                l_run[h] += s[ks][h];
+            }
         }
 
         // Probabilities to LDS, [row][head].
@@ -276,125 +447,147 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(StepArgs a)
         }
         __builtin_amdgcn_wave_barrier();
 
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            acc[h].x *= alpha[h];
-            acc[h].y *= alpha[h];
-            acc[h].z *= alpha[h];
-            acc[h].w *= alpha[h];
-            l_run[h] *= alpha[h];
-        }
-
-        // Weighted V.
+        // Weighted V on the matrix cores: per V load set and float4 component
+        // e, one 4x4x1 MFMA adds p[row][head i] * V[row][4*vj + e] for the
+        // four heads of a quad (A: lane 4b+i gives p of head i for its row;
+        // B: each lane its own V component).
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const int r = vs * RPV + vg;
 #pragma unroll
-            for (int h = 0; h < G; h++) {
-                const float p = p_lds[wave][r * G + h];
-                acc[h].x += p * vb[vs].x;
-                acc[h].y += p * vb[vs].y;
-                acc[h].z += p * vb[vs].z;
-                acc[h].w += p * vb[vs].w;
-                l_run[h] += p;
+            for (int q = 0; q < GQ; q++) {
+                const int h = 4 * q + (lane & 3);
+                const float pa = (h < G) ? p_lds[wave][r * G + h] : 0.0f;
+                acc[q][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].x, acc[q][0], 0, 0, 0);
+                acc[q][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].y, acc[q][1], 0, 0, 0);
+                acc[q][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].z, acc[q][2], 0, 0, 0);
+                acc[q][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].w, acc[q][3], 0, 0, 0);
             }
         }
         __builtin_amdgcn_wave_barrier();
     }
 
-    // Fold the V row groups of the wave, then combine the waves in LDS.
+    // Per-wave partials to LDS: every V row slot its own accumulator.
+#pragma unroll
+    for (int h = 0; h < G; h++)
+        comb_o[wave][vg][h][vj] = make_float4(acc[h / 4][0][h % 4], acc[h / 4][1][h % 4],
+                                              acc[h / 4][2][h % 4], acc[h / 4][3][h % 4]);
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        acc[h].x = xor_sum_above<LPV>(acc[h].x);
-        acc[h].y = xor_sum_above<LPV>(acc[h].y);
-        acc[h].z = xor_sum_above<LPV>(acc[h].z);
-        acc[h].w = xor_sum_above<LPV>(acc[h].w);
-        l_run[h] = xor_sum_above<LPV>(l_run[h]);
-    }
-    if (vg == 0) {
-#pragma unroll
-        for (int h = 0; h < G; h++)
-            *reinterpret_cast<float4 *>(&comb_o[wave][h][4 * vj]) = acc[h];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            comb_ml[wave][h][0] = m_run[h];
-            comb_ml[wave][h][1] = l_run[h];
+        const float lw = groups_sum<LPR>(l_run[h]);
+        if (lane == 0) {
+            comb_l[wave][h] = lw;
+            comb_m[wave][h] = m_ref[h];
         }
     }
     __syncthreads();
 
+    // Combine the waves: one float4 of one head per thread.
     const bool single = (n_chunks == 1);
-    for (int idx = tid; idx < G * HD; idx += kThreads) {
-        const int h = idx / HD, d = idx % HD;
-        float M = -INFINITY;
+    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * kMaxChunks;
+    const uint32_t ws_o_bytes = (uint32_t)G * kMaxChunks * HD * 4u;
+    const uint32_t ws_ml_bytes = (uint32_t)G * kMaxChunks * 8u;
+    const __amdgpu_buffer_rsrc_t wo_rsrc = make_rsrc(a.ws_o + ws_head0 * HD, ws_o_bytes);
+    const __amdgpu_buffer_rsrc_t wm_rsrc = make_rsrc(a.ws_ml + ws_head0, ws_ml_bytes);
+    for (int idx = tid; idx < G * D4; idx += S::THREADS) {
+        const int ch = idx / D4, cd4 = idx % D4;  // head, float4 column
+        float M = -INFINITY, L = 0.f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, comb_ml[w][h][0]);
-        float o = 0.f, L = 0.f;
+        for (int w = 0; w < NW; w++) M = fmaxf(M, comb_m[w][ch]);
 #pragma unroll
-        for (int w = 0; w < kWaves; w++) {
-            const float mw = comb_ml[w][h][0];
+        for (int w = 0; w < NW; w++) {
+            const float mw = comb_m[w][ch];
             const float sc = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - M);
-            o += sc * comb_o[w][h][d];
-            L += sc * comb_ml[w][h][1];
+#pragma unroll
+            for (int r = 0; r < RPV; r++) fma4(o, sc, comb_o[w][r][ch][cd4]);
+            L += sc * comb_l[w][ch];
         }
-        const int qh = kvh * G + h;
         if (single) {
-            a.out[(size_t)seq * q_dim + (size_t)qh * HD + d] = o / L;
+            scale4(o, 1.0f / L);
+            reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + ch) * HD)[cd4] = o;
         } else {
-            const size_t row = ((size_t)seq * a.n_heads + qh) * kMaxChunks + chunk_id;
-            a.ws_o[row * HD + d] = o;
-            if (d == 0) a.ws_ml[row] = make_float2(M, L);
+            // Partial o and (max, sum), into this XCD's L2.
+            const uint32_t row = (uint32_t)ch * kMaxChunks + (uint32_t)chunk_id;
+            buf_store4(wo_rsrc, row * (HD * 4u) + 16u * cd4, o);
+            if (cd4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M, L));
         }
     }
     if (single) return;
 
-    // Arrival: the last chunk of this (sequence, KV head) merges.
-    __threadfence();
+    // Arrival: once this workgroup's partials have reached L2 (stores
+    // drained), count it in with an L2 atomic; the last chunk of this
+    // (sequence, KV head) to arrive merges all of them.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
         int *ctr = a.counters + (size_t)seq * a.n_kv_heads + kvh;
-        const int prev = atomicAdd(ctr, 1);
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         s_last = (prev == n_chunks - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
-    for (int h = wave; h < G; h += kWaves) {
-        const int qh = kvh * G + h;
-        const size_t row0 = ((size_t)seq * a.n_heads + qh) * kMaxChunks;
-        const float2 *ml = a.ws_ml + row0;
-        float M = -INFINITY;
-        for (int c = lane; c < n_chunks; c += kWave) M = fmaxf(M, ml[c].x);
-        M = xor_max_above<1>(M);
-        float L = 0.f;
-        for (int c = lane; c < n_chunks; c += kWave) {
-            const float2 mlc = ml[c];
-            const float mc = mlc.x, lc = mlc.y;
-            const float w = fast_exp2(mc - M);
-            merge_w[wave][c] = w;
-            L += w * lc;
+    // Merge: thread = (head mh, chunk lane mg, float4 column md4); chunk lane
+    // mg folds chunks mg, mg + MG, ... with an online max, B chunks of loads
+    // in flight at a time; the chunk lanes are then combined in LDS.
+    constexpr int B = 16;
+    const int mh = tid / (MG * D4), mg = (tid / D4) % MG, md4 = tid % D4;
+    float mm = -INFINITY, ll = 0.f;
+    float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = mg; c0 < n_chunks; c0 += MG * B) {
+        float2 mlb[B];
+        float4 ob[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const int c = c0 + j * MG;
+            const uint32_t row = (uint32_t)mh * kMaxChunks + (uint32_t)c;
+            // past n_chunks: an offset at the end of the range reads 0
+            mlb[j] = buf_load2<kSc0>(wm_rsrc, c < n_chunks ? row * 8u : ws_ml_bytes);
+            ob[j] = buf_load4<kSc0>(wo_rsrc, c < n_chunks ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
         }
-        L = xor_sum_above<1>(L);
-        __builtin_amdgcn_wave_barrier();
-        const float inv_L = 1.0f / L;
-        constexpr int DPL = HD / kWave;  // dims per lane
-        float o[DPL];
+        float m_new = mm;
 #pragma unroll
-        for (int i = 0; i < DPL; i++) o[i] = 0.f;
-        const float *po = a.ws_o + row0 * HD;
-        for (int c = 0; c < n_chunks; c++) {
-            const float w = merge_w[wave][c];
+        for (int j = 0; j < B; j++)
+            if (c0 + j * MG < n_chunks) m_new = fmaxf(m_new, mlb[j].x);
+        const float al = (mm == -INFINITY) ? 0.f : fast_exp2(mm - m_new);
+        scale4(oo, al);
+        ll *= al;
 #pragma unroll
-            for (int i = 0; i < DPL; i++)
-                o[i] += w * po[(size_t)c * HD + lane + i * kWave];
+        for (int j = 0; j < B; j++) {
+            const float w = (c0 + j * MG < n_chunks) ? fast_exp2(mlb[j].x - m_new) : 0.f;
+            fma4(oo, w, ob[j]);
+            ll += w * mlb[j].y;
         }
+        mm = m_new;
+    }
+    // The chunk lanes meet in LDS (the combine buffers are free again).
+    static_assert(sizeof(comb_o) >= sizeof(float4) * G * MG * D4, "merge scratch");
+    static_assert(sizeof(p_lds) >= sizeof(float) * 2 * G * MG, "merge scratch");
+    float4 *mo = &comb_o[0][0][0][0];      // [G][MG][D4]
+    float *mmx = &p_lds[0][0];             // [G][MG]
+    float *mls = &p_lds[0][0] + G * MG;    // [G][MG]
+    mo[(mh * MG + mg) * D4 + md4] = oo;
+    if (md4 == 0) {
+        mmx[mh * MG + mg] = mm;
+        mls[mh * MG + mg] = ll;
+    }
+    __syncthreads();
+    if (mg == 0) {
+        float Mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < DPL; i++)
-            a.out[(size_t)seq * q_dim + (size_t)qh * HD + lane + i * kWave] = o[i] * inv_L;
-        __builtin_amdgcn_wave_barrier();
+        for (int g = 0; g < MG; g++) Mx = fmaxf(Mx, mmx[mh * MG + g]);
+        float Lx = 0.f;
+        float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int g = 0; g < MG; g++) {
+            const float mgv = mmx[mh * MG + g];
+            const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
+            fma4(ox, sc, mo[(mh * MG + g) * D4 + md4]);
+            Lx += sc * mls[mh * MG + g];
+        }
+        scale4(ox, 1.0f / Lx);
+        reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD)[md4] = ox;
     }
     if (tid == 0) a.counters[(size_t)seq * a.n_kv_heads + kvh] = 0;
 }

@@ -69,10 +69,14 @@ int set_err(leap_hip_attention *h, int code, const char *fmt, ...)
 
 using KernelFn = void (*)(leap::StepArgs);
 
+// Waves per workgroup of the decode kernel.
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * leap::kWave;
+
 KernelFn pick_kernel(int hd, int g)
 {
 #define LEAP_CASE(HD, G) \
-    if (hd == HD && g == G) return leap::decode_attention_kernel<HD, G>;
+    if (hd == HD && g == G) return leap::decode_attention_kernel<HD, G, kWaves>;
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
@@ -94,7 +98,7 @@ int round_up(int x, int q) { return (x + q - 1) / q * q; }
 // chunks per sequence.
 int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
 {
-    const int quantum = leap::rows_per_pass(h->cfg.head_dim);
+    const int quantum = leap::rows_per_pass(h->cfg.head_dim, kWaves);
     const int floor_chunk = round_up((max_T + leap::kMaxChunks - 1) / leap::kMaxChunks, quantum);
     int c;
     if (h->split > 0) {
@@ -105,6 +109,7 @@ int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
         per = std::min<long long>(per, 1 << 20);
         c = round_up((int)per, quantum);
     }
+    c = std::min(c, round_up(max_T, quantum));
     return std::max(c, std::max(floor_chunk, quantum));
 }
 
@@ -138,10 +143,16 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     a.n_heads = h->cfg.n_heads;
     a.n_kv_heads = h->cfg.n_kv_heads;
     a.chunk = chunk;
+    a.grid_chunks = grid_x;
+    a.n_groups = n_seq * h->cfg.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
 
-    hipLaunchKernelGGL(fn, dim3(grid_x, h->cfg.n_kv_heads, n_seq), dim3(leap::kThreads), 0,
-                       stream, a);
+    // Workgroup id = ((group / 8) * grid_x + chunk) * 8 + group % 8, with
+    // group = seq * n_kv_heads + kv_head: a group's chunks share one XCD.
+    const long long n_groups = (long long)n_seq * h->cfg.n_kv_heads;
+    const long long n_wg = (n_groups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
+    if (n_wg > 0x7fffffffLL) return set_err(h, -EINVAL, "launch too large");
+    hipLaunchKernelGGL(fn, dim3((unsigned)n_wg), dim3(kThreads), 0, stream, a);
     HIP_TRY(h, hipGetLastError());
     return 0;
 }
@@ -166,6 +177,13 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
         c.layer_begin >= c.layer_end)
         return set_err(nullptr, -EINVAL, "bad layer range [%d, %d) of %d or seq_len %d",
                        c.layer_begin, c.layer_end, c.n_layers, c.seq_len);
+    // K/V rows are addressed with 32-bit byte offsets inside one (sequence,
+    // layer) slab, with one chunk of slack past seq_len.
+    const unsigned long long slab_bytes =
+        ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, kWaves)) *
+        (unsigned long long)c.n_kv_heads * c.head_dim * sizeof(float);
+    if (slab_bytes >= (1ull << 32))
+        return set_err(nullptr, -EINVAL, "seq_len %d: one layer's cache rows exceed 4 GiB", c.seq_len);
     if (c.max_batch <= 0 || c.max_batch > 65535)
         return set_err(nullptr, -EINVAL, "max_batch %d out of range", c.max_batch);
     if (!(c.rope_theta <= 0.0f || std::isfinite(c.rope_theta)))
@@ -240,8 +258,7 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
 {
     if (!h) return 0;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
-    void *bufs[] = {h->k_cache, h->v_cache, h->rope, h->ws_o, h->ws_ml, h->counters,
-                    h->pos_dev, h->q_dev, h->k_dev, h->v_dev, h->out_dev};
+    void *bufs[] = {h->k_cache, h->v_cache, h->rope, h->ws_o, h->ws_ml, h->counters, h->pos_dev, h->q_dev, h->k_dev, h->v_dev, h->out_dev};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
