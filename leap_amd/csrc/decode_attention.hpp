@@ -12,10 +12,14 @@
 //     128-bit buffer loads, and every wave serves all q heads of the KV group
 //     from those registers: GQA score (:496-630), online softmax (running
 //     max / sum, :216-238) and the weighted-V accumulation (:634-661);
-//   - the merge of the chunk partials: each chunk writes an unnormalised
-//     partial (o, max, sum) to the workspace and counts itself in with an
-//     atomic; the last chunk of a (sequence, KV head) to arrive combines all
-//     partials and resets the counter.
+//   - the merge of the chunk partials, as a two-level arrival tree: each chunk
+//     writes an unnormalised partial (o, max, sum) and counts itself in on its
+//     sub-group's counter (kSubGroup consecutive chunks); the last arrival of a
+//     sub-group folds that sub-group's partials into one record and counts in
+//     on the final counter, whose last arrival folds the sub-group records
+//     into the output.  Each counter sees at most kSubGroup (or kMaxSub)
+//     arrivals and each fold reads a few KB, instead of one workgroup pulling
+//     every partial through a single CU.
 //
 // XCD placement.  Workgroups are dealt to the XCDs round-robin by workgroup
 // id, so id % 8 names the XCD (the same holds within a 1-, 2- or 4-XCD
@@ -35,6 +39,10 @@ namespace leap {
 
 constexpr int kWave = 64;
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
+constexpr int kSubGroup = 8;              // chunks per first-level merge
+constexpr int kMaxSub = kMaxChunks / kSubGroup;
+constexpr int kRecords = kMaxChunks + kMaxSub;  // partial records per head
+constexpr int kCounters = 1 + kMaxSub;          // arrival counters per (sequence, KV head)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc0 = 1;                   // cache policy: bypass L1, read L2
 
@@ -51,9 +59,11 @@ struct StepArgs {
     float *v_cache;
     const float4 *rope;  // [seq_len][HD/4] of (cos_2i, sin_2i, cos_2i+1, sin_2i+1)
     const int *pos_dev;  // per-sequence positions, or nullptr -> pos_scalar
-    float *ws_o;         // [n_seq][n_heads][kMaxChunks][HD] partial outputs
-    float2 *ws_ml;       // [n_seq][n_heads][kMaxChunks] (max, sum) in log2 units
-    int *counters;       // [n_seq][n_kv_heads] arrival counters, zero between launches
+    float *ws_o;         // [n_seq][n_heads][kRecords][HD] partial outputs: chunk
+                         // records, then first-level merge records
+    float2 *ws_ml;       // [n_seq][n_heads][kRecords] (max, sum) in log2 units
+    int *counters;       // [n_seq][n_kv_heads][kCounters] arrival counters (final,
+                         // then one per sub-group), zero between launches
     long long seq_stride;// floats between sequence slabs
     int pos_scalar;
     int max_pos;         // launch was sized for positions <= max_pos
@@ -484,9 +494,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 
     // Combine the waves: one float4 of one head per thread.
     const bool single = (n_chunks == 1);
-    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * kMaxChunks;
-    const uint32_t ws_o_bytes = (uint32_t)G * kMaxChunks * HD * 4u;
-    const uint32_t ws_ml_bytes = (uint32_t)G * kMaxChunks * 8u;
+    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * kRecords;
+    const uint32_t ws_o_bytes = (uint32_t)G * kRecords * HD * 4u;
+    const uint32_t ws_ml_bytes = (uint32_t)G * kRecords * 8u;
     const __amdgpu_buffer_rsrc_t wo_rsrc = make_rsrc(a.ws_o + ws_head0 * HD, ws_o_bytes);
     const __amdgpu_buffer_rsrc_t wm_rsrc = make_rsrc(a.ws_ml + ws_head0, ws_ml_bytes);
     for (int idx = tid; idx < G * D4; idx += S::THREADS) {
@@ -508,88 +518,124 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + ch) * HD)[cd4] = o;
         } else {
             // Partial o and (max, sum), into this XCD's L2.
-            const uint32_t row = (uint32_t)ch * kMaxChunks + (uint32_t)chunk_id;
+            const uint32_t row = (uint32_t)ch * kRecords + (uint32_t)chunk_id;
             buf_store4(wo_rsrc, row * (HD * 4u) + 16u * cd4, o);
             if (cd4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M, L));
         }
     }
     if (single) return;
 
-    // Arrival: once this workgroup's partials have reached L2 (stores
-    // drained), count it in with an L2 atomic; the last chunk of this
-    // (sequence, KV head) to arrive merges all of them.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        int *ctr = a.counters + (size_t)seq * a.n_kv_heads + kvh;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        s_last = (prev == n_chunks - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-
-    // Merge: thread = (head mh, chunk lane mg, float4 column md4); chunk lane
-    // mg folds chunks mg, mg + MG, ... with an online max, B chunks of loads
-    // in flight at a time; the chunk lanes are then combined in LDS.
-    constexpr int B = 16;
+    // Fold records [first, first + n) of the G heads: thread = (head mh,
+    // record lane mg, float4 column md4); record lane mg takes records
+    // first + mg, first + mg + MG, ... with an online max, eight records of
+    // loads in flight at a time (L2 reads), then the record lanes meet in LDS.
+    // Leaves (o, M, L) of head mh, columns md4, in the threads with mg == 0.
     const int mh = tid / (MG * D4), mg = (tid / D4) % MG, md4 = tid % D4;
-    float mm = -INFINITY, ll = 0.f;
-    float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = mg; c0 < n_chunks; c0 += MG * B) {
-        float2 mlb[B];
-        float4 ob[B];
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            const int c = c0 + j * MG;
-            const uint32_t row = (uint32_t)mh * kMaxChunks + (uint32_t)c;
-            // past n_chunks: an offset at the end of the range reads 0
-            mlb[j] = buf_load2<kSc0>(wm_rsrc, c < n_chunks ? row * 8u : ws_ml_bytes);
-            ob[j] = buf_load4<kSc0>(wo_rsrc, c < n_chunks ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
-        }
-        float m_new = mm;
-#pragma unroll
-        for (int j = 0; j < B; j++)
-            if (c0 + j * MG < n_chunks) m_new = fmaxf(m_new, mlb[j].x);
-        const float al = (mm == -INFINITY) ? 0.f : fast_exp2(mm - m_new);
-        scale4(oo, al);
-        ll *= al;
-#pragma unroll
-        for (int j = 0; j < B; j++) {
-            const float w = (c0 + j * MG < n_chunks) ? fast_exp2(mlb[j].x - m_new) : 0.f;
-            fma4(oo, w, ob[j]);
-            ll += w * mlb[j].y;
-        }
-        mm = m_new;
-    }
-    // The chunk lanes meet in LDS (the combine buffers are free again).
     static_assert(sizeof(comb_o) >= sizeof(float4) * G * MG * D4, "merge scratch");
     static_assert(sizeof(p_lds) >= sizeof(float) * 2 * G * MG, "merge scratch");
     float4 *mo = &comb_o[0][0][0][0];      // [G][MG][D4]
     float *mmx = &p_lds[0][0];             // [G][MG]
     float *mls = &p_lds[0][0] + G * MG;    // [G][MG]
-    mo[(mh * MG + mg) * D4 + md4] = oo;
-    if (md4 == 0) {
-        mmx[mh * MG + mg] = mm;
-        mls[mh * MG + mg] = ll;
+    auto fold = [&](int first, int n, float4 &ox, float &Mx, float &Lx) {
+        constexpr int B = 8;
+        float mm = -INFINITY, ll = 0.f;
+        float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c0 = mg; c0 < n; c0 += MG * B) {
+            float2 mlb[B];
+            float4 ob[B];
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                const int c = c0 + j * MG;
+                const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
+                // past n: an offset at the end of the range reads 0
+                mlb[j] = buf_load2<kSc0>(wm_rsrc, c < n ? row * 8u : ws_ml_bytes);
+                ob[j] = buf_load4<kSc0>(wo_rsrc, c < n ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
+            }
+            float m_new = mm;
+#pragma unroll
+            for (int j = 0; j < B; j++)
+                if (c0 + j * MG < n) m_new = fmaxf(m_new, mlb[j].x);
+            const float al = (mm == -INFINITY) ? 0.f : fast_exp2(mm - m_new);
+            scale4(oo, al);
+            ll *= al;
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                const float w = (c0 + j * MG < n) ? fast_exp2(mlb[j].x - m_new) : 0.f;
+                fma4(oo, w, ob[j]);
+                ll += w * mlb[j].y;
+            }
+            mm = m_new;
+        }
+        __syncthreads();  // LDS scratch is free (combine buffers / earlier fold)
+        mo[(mh * MG + mg) * D4 + md4] = oo;
+        if (md4 == 0) {
+            mmx[mh * MG + mg] = mm;
+            mls[mh * MG + mg] = ll;
+        }
+        __syncthreads();
+        if (mg == 0) {
+            Mx = -INFINITY;
+#pragma unroll
+            for (int g = 0; g < MG; g++) Mx = fmaxf(Mx, mmx[mh * MG + g]);
+            Lx = 0.f;
+            ox = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int g = 0; g < MG; g++) {
+                const float mgv = mmx[mh * MG + g];
+                const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
+                fma4(ox, sc, mo[(mh * MG + g) * D4 + md4]);
+                Lx += sc * mls[mh * MG + g];
+            }
+        }
+    };
+    int *ctr = a.counters + ((size_t)seq * a.n_kv_heads + kvh) * kCounters;
+    float4 *out_row = reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD);
+
+    // Level 1: once this workgroup's partials have reached L2 (stores
+    // drained), count it in on its sub-group's counter (an L2 atomic).
+    const int sg = chunk_id / kSubGroup;
+    const int n_sg = (n_chunks + kSubGroup - 1) / kSubGroup;
+    const int sg_n = min(kSubGroup, n_chunks - sg * kSubGroup);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(ctr + 1 + sg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        s_last = (prev == sg_n - 1);
     }
     __syncthreads();
-    if (mg == 0) {
-        float Mx = -INFINITY;
-#pragma unroll
-        for (int g = 0; g < MG; g++) Mx = fmaxf(Mx, mmx[mh * MG + g]);
-        float Lx = 0.f;
-        float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int g = 0; g < MG; g++) {
-            const float mgv = mmx[mh * MG + g];
-            const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
-            fma4(ox, sc, mo[(mh * MG + g) * D4 + md4]);
-            Lx += sc * mls[mh * MG + g];
+    if (!s_last) return;
+    if (tid == 0) ctr[1 + sg] = 0;
+    float4 ox;
+    float Mx, Lx;
+    fold(sg * kSubGroup, sg_n, ox, Mx, Lx);
+    if (n_sg == 1) {
+        if (mg == 0) {
+            scale4(ox, 1.0f / Lx);
+            out_row[md4] = ox;
         }
-        scale4(ox, 1.0f / Lx);
-        reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD)[md4] = ox;
+        return;
     }
-    if (tid == 0) a.counters[(size_t)seq * a.n_kv_heads + kvh] = 0;
+    if (mg == 0) {
+        const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(kMaxChunks + sg);
+        buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, ox);
+        if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(Mx, Lx));
+    }
+
+    // Level 2: the last sub-group to finish folds the sub-group records.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        s_last = (prev == n_sg - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) ctr[0] = 0;
+    fold(kMaxChunks, n_sg, ox, Mx, Lx);
+    if (mg == 0) {
+        scale4(ox, 1.0f / Lx);
+        out_row[md4] = ox;
+    }
 }
 
 // ---- synthetic data ---------------------------------------------------------

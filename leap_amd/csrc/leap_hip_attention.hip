@@ -237,10 +237,10 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMemcpyAsync(h->rope, packed.data(), packed.size() * sizeof(float),
                               hipMemcpyHostToDevice, h->stream));
 
-    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::kMaxChunks;
+    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::kRecords;
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads;
+    const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters;
     CREATE_TRY(hipMalloc(&h->counters, n_ctr * sizeof(int)));
     CREATE_TRY(hipMemsetAsync(h->counters, 0, n_ctr * sizeof(int), h->stream));
     CREATE_TRY(hipMalloc(&h->pos_dev, (size_t)c.max_batch * sizeof(int)));
