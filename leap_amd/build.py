@@ -19,6 +19,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libleap_hip_attention.so")
+DEMO = os.path.join(PKG, "host", "engine_demo")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -59,6 +60,15 @@ def build(verbose: bool = False) -> str:
             print(" ".join(cmd))
         _run(cmd)
     os.replace(LIB + ".tmp", LIB)
+    # the C++20 engine-side wrapper and demo layer loop, linked against the
+    # library in place
+    demo = ["g++", "-std=c++20", "-O2", "-Wall", "-I", INCLUDE, "-I", os.path.join(PKG, "host"),
+            os.path.join(PKG, "host", "engine_demo.cpp"), "-o", DEMO + ".tmp", "-L", PKG,
+            "-lleap_hip_attention", "-Wl,-rpath,$ORIGIN/.."]
+    if verbose:
+        print(" ".join(demo))
+    _run(demo)
+    os.replace(DEMO + ".tmp", DEMO)
     return LIB
 
 

@@ -1,0 +1,77 @@
+// C++20 engine-side wrapper of the leap_hip_attention C ABI.
+//
+// This is the thin layer a LEAP engine (src/inference/FloatTransformer.cpp or
+// QuantizedTransformer.cpp) keeps around the shim: it owns one handle, turns
+// negative status codes into std::runtime_error the way the engine reports
+// its own failures (TransformerFactory.cpp:59-135 throws runtime_error), and
+// exposes the attention block of run_layer (FloatTransformer.cpp:396-662) as
+// one call.
+#pragma once
+
+#include <cstdint>
+#include <span>
+#include <stdexcept>
+#include <string>
+#include <utility>
+
+#include "leap_hip_attention.h"
+
+namespace leap {
+
+class HipAttention {
+public:
+    struct Dims {
+        int n_layers, layer_begin, layer_end, n_heads, n_kv_heads, head_dim, seq_len;
+        float rope_theta = 500000.0f;  // FloatTransformer.cpp:65
+        int max_batch = 1;
+        int device = 0;
+    };
+
+    explicit HipAttention(const Dims &d)
+    {
+        const leap_hip_attention_config c{d.n_layers, d.layer_begin, d.layer_end, d.n_heads,
+                                          d.n_kv_heads, d.head_dim,    d.seq_len,   d.rope_theta,
+                                          d.max_batch,  d.device};
+        check(leap_hip_attention_create(&c, &h_), nullptr);
+        q_dim_ = d.n_heads * d.head_dim;
+        kv_dim_ = d.n_kv_heads * d.head_dim;
+    }
+    HipAttention(const HipAttention &) = delete;
+    HipAttention &operator=(const HipAttention &) = delete;
+    HipAttention(HipAttention &&o) noexcept : h_(std::exchange(o.h_, nullptr)), q_dim_(o.q_dim_), kv_dim_(o.kv_dim_) {}
+    ~HipAttention() { leap_hip_attention_destroy(h_); }
+
+    // The attention block of run_layer(l, pos, x): q is s->q (pre-RoPE),
+    // k_new / v_new the k and v GEMV outputs, out receives s->xb.
+    void step(int layer, int pos, std::span<const float> q, std::span<const float> k_new,
+              std::span<const float> v_new, std::span<float> out)
+    {
+        if ((int)q.size() != q_dim_ || (int)out.size() != q_dim_ || (int)k_new.size() != kv_dim_ ||
+            (int)v_new.size() != kv_dim_)
+            throw std::invalid_argument("HipAttention::step: buffer sizes do not match the model");
+        check(leap_hip_attention_step(h_, layer, pos, q.data(), k_new.data(), v_new.data(), out.data()), h_);
+    }
+
+    // clear_kv_cache (FloatTransformer.cpp:74-77).
+    void clear_kv_cache() { check(leap_hip_attention_clear(h_), h_); }
+
+    void kv_download(int seq, int layer, int pos_begin, int pos_end, float *k, float *v)
+    {
+        check(leap_hip_attention_kv_download(h_, seq, layer, pos_begin, pos_end, k, v), h_);
+    }
+
+    leap_hip_attention *handle() const { return h_; }
+
+private:
+    static void check(int rc, const leap_hip_attention *h)
+    {
+        if (rc != 0)
+            throw std::runtime_error(std::string("leap_hip_attention: ") + leap_hip_attention_last_error(h) +
+                                     " (status " + std::to_string(rc) + ")");
+    }
+
+    leap_hip_attention *h_ = nullptr;
+    int q_dim_ = 0, kv_dim_ = 0;
+};
+
+}  // namespace leap

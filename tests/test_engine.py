@@ -1,0 +1,49 @@
+"""The C++20 engine-side wrapper and demo layer loop (leap_amd/host)."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.conftest import gpu_available
+from tests.helpers import assert_close
+
+DEMO = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "leap_amd", "host",
+                    "engine_demo")
+
+
+def _demo():
+    if not os.path.isfile(DEMO):
+        pytest.fail(f"{DEMO} missing: build with `python -m leap_amd.build`")
+    return DEMO
+
+
+def test_engine_demo_usage_error():
+    r = subprocess.run([_demo()], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
+
+
+def test_engine_demo_reports_shim_errors_as_exceptions(tmp_path):
+    if gpu_available():
+        pytest.skip("a GPU is present")
+    r = subprocess.run([_demo(), "2", "8", "2", "64", "16", "4", str(tmp_path)], capture_output=True,
+                       text=True)
+    assert r.returncode == 3 and "no HIP device" in r.stderr
+
+
+@pytest.mark.gpu
+def test_engine_demo_decode_matches_oracle(tmp_path, hip_device):
+    L, nh, nkv, hd, seq_len, n_tok = 2, 16, 4, 128, 200, 150
+    r = subprocess.run([_demo(), str(L), str(nh), str(nkv), str(hd), str(seq_len), str(n_tok),
+                        str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rec = nh * hd * 2 + nkv * hd * 2
+    trace = np.fromfile(tmp_path / "trace.bin", dtype=np.float32).reshape(n_tok, L, rec)
+    orc = O.Oracle(L, nh, nkv, hd, seq_len)
+    for pos in range(n_tok):
+        for layer in range(L):
+            t = trace[pos, layer]
+            q, k, v, xb = np.split(t, [nh * hd, nh * hd + nkv * hd, nh * hd + 2 * nkv * hd])
+            want, _ = orc.step(layer, pos, q, k, v)
+            assert_close(xb, want, what=f"token {pos} layer {layer}")
