@@ -223,17 +223,6 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 // ---- the fused decode-attention kernel --------------------------------------
 
-// Rotation for q: fused multiply-adds are fine here (q is not stored).
-__device__ __forceinline__ float4 rope4_fma(float4 x, float4 t)
-{
-    float4 r;
-    r.x = x.x * t.x - x.y * t.y;
-    r.y = x.y * t.x + x.x * t.y;
-    r.z = x.z * t.z - x.w * t.w;
-    r.w = x.w * t.z + x.z * t.w;
-    return r;
-}
-
 // Growth of the running max (log2 units) tolerated before the accumulators
 // are rescaled: p = 2^(s - m_ref) stays below 2^kLazyMax.
 constexpr float kLazyMax = 8.0f;
@@ -298,6 +287,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const float4 *rope_row = a.rope + (size_t)pos * (HD / 4);
 
     __shared__ float p_lds[NW][R * G];
+    __shared__ float4 q_lds[G][HD / 4];  // rotated, scaled q of the group's heads
     __shared__ float4 comb_o[NW][RPV][G][D4];
     __shared__ float comb_l[NW][G];
     __shared__ float comb_m[NW][G];
@@ -308,22 +298,36 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // V layout: lane = vg*LPV + vj; lane holds dims 4*vj .. +3.
     const int vg = lane / LPV, vj = lane % LPV;
 
-    // Issue order: q, table row and the new token's k / v first, then the
-    // first K/V tile, so that rotating q waits only for the small loads.
-    float4 qr[G][NF], tab[NF], knew[NF];
-#pragma unroll
-    for (int f = 0; f < NF; f++) {
-        const int d4 = f * LPR + kj;
-        tab[f] = rope_row[d4];
-        knew[f] = *reinterpret_cast<const float4 *>(k_row_new + 4 * d4);
-#pragma unroll
-        for (int h = 0; h < G; h++)
-            qr[h][f] = *reinterpret_cast<const float4 *>(qg + (size_t)h * HD + 4 * d4);
-    }
-    const float4 vnew = *reinterpret_cast<const float4 *>(v_row_new + 4 * vj);
-
+    // Prologue.  The group's q heads are loaded once per workgroup (one pair
+    // per thread) ahead of the first K/V tile, rotated with the score scale
+    // folded in, and shared through LDS; only the workgroup whose chunk holds
+    // pos loads and rotates the new token's k and v.
     const int chunk_begin = chunk_id * a.chunk;
     const int n_sub = a.chunk / S::ROWS;
+    const bool has_pos = (chunk_id == n_chunks - 1);
+    constexpr int PAIRS = G * HD / 2;
+    constexpr int QP = (PAIRS + S::THREADS - 1) / S::THREADS;  // q pairs per thread
+    const float2 *rope2 = reinterpret_cast<const float2 *>(rope_row);
+    float2 qp[QP], qt[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int pair = tid + i * S::THREADS;
+        if (pair < PAIRS) {
+            qp[i] = reinterpret_cast<const float2 *>(qg)[pair];
+            qt[i] = rope2[pair % (HD / 2)];
+        }
+    }
+    float4 tab[NF], knew[NF];
+    float4 vnew = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (has_pos) {
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+            const int d4 = f * LPR + kj;
+            tab[f] = rope_row[d4];
+            knew[f] = *reinterpret_cast<const float4 *>(k_row_new + 4 * d4);
+        }
+        vnew = *reinterpret_cast<const float4 *>(v_row_new + 4 * vj);
+    }
 
     float4 kb[KS][NF], vb[VS];
     auto load_tile = [&](int sub) {
@@ -344,17 +348,29 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 
     load_tile(0);
 
-    // k exactly as the reference rotates it (it is stored); q with the
-    // score scale folded in, so scores come out in log2 units.
+    // q: rotate (fused multiply-adds are fine, q is not stored) and scale so
+    // scores come out in log2 units; k: exactly as the reference rotates it,
+    // since it is stored.
+    float *q_flat = reinterpret_cast<float *>(&q_lds[0][0]);
 #pragma unroll
-    for (int f = 0; f < NF; f++) {
-        knew[f] = rope4(knew[f], tab[f]);
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            qr[h][f] = rope4_fma(qr[h][f], tab[f]);
-            scale4(qr[h][f], a.scale_log2);
+    for (int i = 0; i < QP; i++) {
+        const int pair = tid + i * S::THREADS;
+        if (pair < PAIRS) {
+            const float x0 = qp[i].x, x1 = qp[i].y, c = qt[i].x, sn = qt[i].y;
+            q_flat[2 * pair] = (x0 * c - x1 * sn) * a.scale_log2;
+            q_flat[2 * pair + 1] = (x1 * c + x0 * sn) * a.scale_log2;
         }
     }
+    if (has_pos) {
+#pragma unroll
+        for (int f = 0; f < NF; f++) knew[f] = rope4(knew[f], tab[f]);
+    }
+    __syncthreads();
+    float4 qr[G][NF];
+#pragma unroll
+    for (int f = 0; f < NF; f++)
+#pragma unroll
+        for (int h = 0; h < G; h++) qr[h][f] = q_lds[h][f * LPR + kj];
 
     // P.V accumulators, MFMA 4x4x1 (16 blocks) layout: block b = lane / 4
     // covers the lanes of one V row; acc[q][e][i] is head 4q+i at dim
