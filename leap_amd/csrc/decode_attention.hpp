@@ -7,7 +7,7 @@
 //   - the KV append: the workgroup whose chunk holds `pos` rotates k_new,
 //     stores k_new / v_new into cache[layer][pos] and uses them in registers;
 //   - split-K flash decoding over the positions [0, pos]: a workgroup owns one
-//     (sequence, KV head, chunk of positions); its eight waves stream
+//     (sequence, KV head, chunk of positions); its waves stream
 //     interleaved sub-tiles of K and V rows straight into registers with
 //     128-bit buffer loads, and every wave serves all q heads of the KV group
 //     from those registers: GQA score (:496-630), online softmax (running
@@ -46,9 +46,13 @@ constexpr int kCounters = 1 + kMaxSub;          // arrival counters per (sequenc
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc0 = 1;                   // cache policy: bypass L1, read L2
 
-// Positions one workgroup pass covers with NW waves (NW sub-tiles of 2048/HD
-// rows); chunk sizes are multiples of it.
-__host__ __device__ constexpr int rows_per_pass(int hd, int nw) { return nw * (2048 / hd); }
+// Rows of one wave sub-tile: 16 KiB of K and V for up to four q heads per KV
+// head, half that for eight (their scores and q take twice the registers).
+__host__ __device__ constexpr int subtile_rows(int hd, int g) { return (g >= 8 ? 1024 : 2048) / hd; }
+
+// Positions one workgroup pass covers with NW waves; chunk sizes are
+// multiples of it.
+__host__ __device__ constexpr int rows_per_pass(int hd, int g, int nw) { return nw * subtile_rows(hd, g); }
 
 struct StepArgs {
     const float *q;      // [n_seq][n_heads*HD], pre-RoPE
@@ -70,7 +74,7 @@ struct StepArgs {
     int seq_len;
     int n_heads;
     int n_kv_heads;
-    int chunk;           // positions per workgroup, multiple of rows_per_pass(HD, NW)
+    int chunk;           // positions per workgroup, multiple of rows_per_pass(HD, G, NW)
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
@@ -233,7 +237,7 @@ struct Shape {
     static constexpr int LPR = (HD * G >= 1024) ? 16 : 8;  // lanes per K row
     static constexpr int NF = HD / (4 * LPR);              // float4 per lane per K row
     static constexpr int RPK = kWave / LPR;                // K rows per load set
-    static constexpr int R = 2048 / HD;                    // rows per wave sub-tile
+    static constexpr int R = subtile_rows(HD, G);          // rows per wave sub-tile
     static constexpr int KS = R / RPK;                     // K load sets per sub-tile
     static constexpr int LPV = HD / 4;                     // lanes per V row
     static constexpr int RPV = kWave / LPV;                // V rows per load set

@@ -98,7 +98,7 @@ int round_up(int x, int q) { return (x + q - 1) / q * q; }
 // chunks per sequence.
 int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
 {
-    const int quantum = leap::rows_per_pass(h->cfg.head_dim, kWaves);
+    const int quantum = leap::rows_per_pass(h->cfg.head_dim, h->group, kWaves);
     const int floor_chunk = round_up((max_T + leap::kMaxChunks - 1) / leap::kMaxChunks, quantum);
     int c;
     if (h->split > 0) {
@@ -180,7 +180,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     // K/V rows are addressed with 32-bit byte offsets inside one (sequence,
     // layer) slab, with one chunk of slack past seq_len.
     const unsigned long long slab_bytes =
-        ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, kWaves)) *
+        ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, 1, kWaves)) *
         (unsigned long long)c.n_kv_heads * c.head_dim * sizeof(float);
     if (slab_bytes >= (1ull << 32))
         return set_err(nullptr, -EINVAL, "seq_len %d: one layer's cache rows exceed 4 GiB", c.seq_len);
