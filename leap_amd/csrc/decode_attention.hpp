@@ -42,13 +42,14 @@ constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV he
 constexpr int kSubGroup = 8;              // chunks per first-level merge
 constexpr int kMaxSub = kMaxChunks / kSubGroup;
 constexpr int kRecords = kMaxChunks + kMaxSub;  // partial records per head
-constexpr int kCounters = 1 + kMaxSub;          // arrival counters per (sequence, KV head)
+constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
+constexpr int kCounters = (1 + kMaxSub) * kCtrStride;  // counter words per (sequence, KV head)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
-constexpr int kSc0 = 1;                   // cache policy: bypass L1, read L2
+constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 
-// Rows of one wave sub-tile: 16 KiB of K and V for up to four q heads per KV
-// head, half that for eight (their scores and q take twice the registers).
-__host__ __device__ constexpr int subtile_rows(int hd, int g) { return (g >= 8 ? 1024 : 2048) / hd; }
+// Rows of one wave sub-tile: 16 KiB of K and V (8 KiB each), whatever the
+// number of q heads per KV head.
+__host__ __device__ constexpr int subtile_rows(int hd, int g) { return (void)g, 2048 / hd; }
 
 // Positions one workgroup pass covers with NW waves; chunk sizes are
 // multiples of it.
@@ -67,7 +68,7 @@ struct StepArgs {
                          // records, then first-level merge records
     float2 *ws_ml;       // [n_seq][n_heads][kRecords] (max, sum) in log2 units
     int *counters;       // [n_seq][n_kv_heads][kCounters] arrival counters (final,
-                         // then one per sub-group), zero between launches
+                         // then one per sub-group, kCtrStride apart), zero between launches
     long long seq_stride;// floats between sequence slabs
     int pos_scalar;
     int max_pos;         // launch was sized for positions <= max_pos
@@ -130,12 +131,15 @@ __device__ __forceinline__ void buf_store2(__amdgpu_buffer_rsrc_t r, uint32_t of
 
 // ---- wave helpers ---------------------------------------------------------
 //
-// Cross-lane reductions use DPP (fused into the VALU op) inside 16-lane rows:
-// quad_perm [1,0,3,2] and [2,3,0,1] exchange lanes differing in bit 0 and
-// bit 1; once values agree inside each quad (or 8-lane half row),
-// row_half_mirror (or row_mirror) brings in the other quad (or half row).
-// Across rows, the four row leaders are read with v_readlane, which leaves a
-// wave-uniform result.
+// The q.K scores come out of 4x4x1 MFMAs with lane = 32*kq + 4*ksl + kj
+// holding the partial dot product of K row 4*kq + kj over dim slice ksl
+// (eight slices).  The slices are summed with DPP inside each 16-lane row
+// (row_ror by 4 and by 8 lanes add the lanes of equal kj) and then across the
+// row pair with v_permlane16_swap, which hands row 0 to row 1 and row 2 to
+// row 3: rows 1 and 3 (lanes 16-31 and 48-63) end up holding the finished
+// scores, rows 0 and 2 hold nothing useful.  The wave max / sum over those
+// rows takes the quad (kj) with DPP and the two rows with v_readlane, which
+// leaves a wave-uniform result.
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x)
@@ -149,48 +153,48 @@ __device__ __forceinline__ float lane_value(float x, int lane)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }
 
-// Sum over the aligned group of W lanes (W = 1..16), result in every lane.
-template <int W>
-__device__ __forceinline__ float group_sum(float x)
+// Odd 16-lane rows receive the even row before them (the first result of
+// v_permlane16_swap with both operands x; the second result is not used).
+__device__ __forceinline__ float from_even_row(float x)
 {
-    if constexpr (W >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
-    if constexpr (W >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
-    if constexpr (W >= 8) x += dpp<0x141>(x);  // row_half_mirror
-    if constexpr (W >= 16) x += dpp<0x140>(x); // row_mirror
-    static_assert(W <= 16, "group_sum covers one row");
-    return x;
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_permlane16_swap(u, u, false, false)[0]);
 }
 
-// Max / sum over the wave of values that are uniform inside each aligned
-// group of FROM lanes (FROM = 1, 2, 4, 8 or 16); the result is wave-uniform.
-template <int FROM>
-__device__ __forceinline__ float groups_max(float x)
+// Sum of the eight dim slices of a score: valid in rows 1 and 3.
+__device__ __forceinline__ float slice_sum(float x)
 {
-    if constexpr (FROM < 16) {
-        if constexpr (FROM <= 1) x = fmaxf(x, dpp<0xB1>(x));
-        if constexpr (FROM <= 2) x = fmaxf(x, dpp<0x4E>(x));
-        if constexpr (FROM <= 4) x = fmaxf(x, dpp<0x141>(x));
-        x = fmaxf(x, dpp<0x140>(x));
-    }
-    return fmaxf(fmaxf(lane_value(x, 0), lane_value(x, 16)),
-                 fmaxf(lane_value(x, 32), lane_value(x, 48)));
+    x += dpp<0x124>(x);  // row_ror:4
+    x += dpp<0x128>(x);  // row_ror:8
+    return x + from_even_row(x);
 }
 
-template <int FROM>
-__device__ __forceinline__ float groups_sum(float x)
+// Max / sum over the score lanes (rows 1 and 3) of a value that is uniform
+// across the eight slice lanes of each K row; wave-uniform result.
+__device__ __forceinline__ float score_rows_max(float x)
 {
-    if constexpr (FROM < 16) {
-        if constexpr (FROM <= 1) x += dpp<0xB1>(x);
-        if constexpr (FROM <= 2) x += dpp<0x4E>(x);
-        if constexpr (FROM <= 4) x += dpp<0x141>(x);
-        x += dpp<0x140>(x);
-    }
-    return (lane_value(x, 0) + lane_value(x, 16)) + (lane_value(x, 32) + lane_value(x, 48));
+    x = fmaxf(x, dpp<0xB1>(x));  // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp<0x4E>(x));  // quad_perm [2,3,0,1]
+    return fmaxf(lane_value(x, 16), lane_value(x, 48));
 }
 
-__device__ __forceinline__ float dot4(float4 a, float4 b)
+__device__ __forceinline__ float score_rows_sum(float x)
 {
-    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    return lane_value(x, 16) + lane_value(x, 48);
+}
+
+// acc += a[c] * b[c] for the four float4 components, one 4x4x1 MFMA each:
+// block k = lane / 4 adds A_k (4x1, lane 4k+i gives row i) times B_k (1x4,
+// lane 4k+j gives column j) to its 4x4 tile, held as column j in lane 4k+j.
+__device__ __forceinline__ f32x4 mfma4(float4 a, float4 b, f32x4 acc)
+{
+    acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_4x4x1f32(a.w, b.w, acc, 0, 0, 0);
+    return acc;
 }
 
 __device__ __forceinline__ void fma4(float4 &acc, float p, float4 v)
@@ -234,20 +238,19 @@ constexpr float kLazyMax = 8.0f;
 template <int HD, int G, int NW>
 struct Shape {
     static constexpr int THREADS = NW * kWave;
-    static constexpr int LPR = (HD * G >= 1024) ? 16 : 8;  // lanes per K row
-    static constexpr int NF = HD / (4 * LPR);              // float4 per lane per K row
-    static constexpr int RPK = kWave / LPR;                // K rows per load set
+    static constexpr int GQ = (G + 3) / 4;                 // head quads (MFMA tile rows)
+    static constexpr int NF = HD / 32;                     // K float4 per lane per row set
     static constexpr int R = subtile_rows(HD, G);          // rows per wave sub-tile
-    static constexpr int KS = R / RPK;                     // K load sets per sub-tile
+    static constexpr int KS = R / 8;                       // K row sets (8 rows) per sub-tile
     static constexpr int LPV = HD / 4;                     // lanes per V row
     static constexpr int RPV = kWave / LPV;                // V rows per load set
     static constexpr int VS = R / RPV;                     // V load sets per sub-tile
     static constexpr int ROWS = NW * R;                    // positions per workgroup pass
     static constexpr int D4 = HD / 4;                      // float4 per head row
     static constexpr int MG = THREADS / (G * D4);          // merge: chunk lanes per head
-    static_assert(HD % (4 * LPR) == 0, "head_dim vs lanes per row");
-    static_assert(R % RPK == 0 && R % RPV == 0, "sub-tile shape");
-    static_assert(G <= LPR, "group size vs lanes per row");
+    static_assert(HD % 32 == 0, "head_dim vs K slices");
+    static_assert(R % 8 == 0 && R % RPV == 0, "sub-tile shape");
+    static_assert(G <= 8, "q heads per KV head");
     static_assert(MG >= 1 && THREADS % (G * D4) == 0, "merge layout");
 };
 
@@ -255,7 +258,7 @@ template <int HD, int G, int NW>
 __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
-    constexpr int LPR = S::LPR, NF = S::NF, RPK = S::RPK, R = S::R, KS = S::KS;
+    constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
     constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, MG = S::MG;
 
     // id = ((group / 8) * grid_chunks + chunk) * 8 + group % 8
@@ -290,15 +293,22 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const float *qg = a.q + (size_t)seq * q_dim + (size_t)kvh * G * HD;
     const float4 *rope_row = a.rope + (size_t)pos * (HD / 4);
 
-    __shared__ float p_lds[NW][R * G];
+    __shared__ __align__(16) float p_lds[NW][R * G];
     __shared__ float4 q_lds[G][HD / 4];  // rotated, scaled q of the group's heads
     __shared__ float4 comb_o[NW][RPV][G][D4];
     __shared__ float comb_l[NW][G];
     __shared__ float comb_m[NW][G];
     __shared__ int s_last;
 
-    // K layout: lane = kg*LPR + kj; lane holds dims 4*(f*LPR + kj) .. +3.
-    const int kg = lane / LPR, kj = lane % LPR;
+    // K layout, for the score MFMAs: lane = 32*kq + 4*ksl + kj holds row
+    // krow = 4*kq + kj of each 8-row set, dims 32*f + 4*ksl .. +3 for
+    // f < HD/32, so one load instruction reads 128 contiguous bytes of each of
+    // eight rows.  MFMA block lane/4 = 8*kq + ksl multiplies four q heads
+    // (A: lane 4*block + i gives head 4*quad + i) by its four rows (B) at one
+    // dim; the eight slices are summed afterwards (slice_sum).
+    const int kj = lane & 3, ksl = (lane >> 2) & 7, kq = lane >> 5;
+    const int krow = 4 * kq + kj;
+    const bool score_lane = (lane >> 4) & 1;  // rows 1 and 3 of the wave
     // V layout: lane = vg*LPV + vj; lane holds dims 4*vj .. +3.
     const int vg = lane / LPV, vj = lane % LPV;
 
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     if (has_pos) {
 #pragma unroll
         for (int f = 0; f < NF; f++) {
-            const int d4 = f * LPR + kj;
+            const int d4 = 8 * f + ksl;
             tab[f] = rope_row[d4];
             knew[f] = *reinterpret_cast<const float4 *>(k_row_new + 4 * d4);
         }
@@ -338,10 +348,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         const int base = chunk_begin + (sub * NW + wave) * R;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const uint32_t roff = (uint32_t)(base + ks * RPK + kg) * row_bytes;
+            const uint32_t roff = (uint32_t)(base + ks * 8 + krow) * row_bytes;
 #pragma unroll
             for (int f = 0; f < NF; f++)
-                kb[ks][f] = buf_load4(k_rsrc, roff + 16u * (uint32_t)(f * LPR + kj));
+                kb[ks][f] = buf_load4(k_rsrc, roff + 16u * (uint32_t)(8 * f + ksl));
         }
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
@@ -370,16 +380,18 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         for (int f = 0; f < NF; f++) knew[f] = rope4(knew[f], tab[f]);
     }
     __syncthreads();
-    float4 qr[G][NF];
+    // Score MFMA A operand: head 4*quad + kj at this lane's dims (zero for
+    // the unused heads of a partial quad).
+    float4 qa[GQ][NF];
 #pragma unroll
-    for (int f = 0; f < NF; f++)
+    for (int qd = 0; qd < GQ; qd++)
 #pragma unroll
-        for (int h = 0; h < G; h++) qr[h][f] = q_lds[h][f * LPR + kj];
+        for (int f = 0; f < NF; f++)
+            qa[qd][f] = (4 * qd + kj < G) ? q_lds[4 * qd + kj][8 * f + ksl] : make_float4(0.f, 0.f, 0.f, 0.f);
 
     // P.V accumulators, MFMA 4x4x1 (16 blocks) layout: block b = lane / 4
     // covers the lanes of one V row; acc[q][e][i] is head 4q+i at dim
     // 4*vj + e of the rows this lane's half (or quarter) of the wave sees.
-    constexpr int GQ = (G + 3) / 4;
     float m_ref[G], l_run[G];
     f32x4 acc[GQ][4];
 #pragma unroll
@@ -400,12 +412,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         // loads, and are appended to cache[layer][pos].
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const int t = base + ks * RPK + kg;
+            const int t = base + ks * 8 + krow;
             if (t == pos) {
 #pragma unroll
                 for (int f = 0; f < NF; f++) {
                     kb[ks][f] = knew[f];
-                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (f * LPR + kj)) = knew[f];
+                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = knew[f];
                 }
             }
         }
@@ -418,18 +430,23 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             }
         }
 
-        // Scores (log2 units) for the KS rows this lane group holds.
+        // Scores (log2 units) on the matrix cores: s[ks][h] is head h at row
+        // ks*8 + krow in the score lanes, -inf elsewhere and past pos.
         float s[KS][G];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const int t = base + ks * RPK + kg;
+            const bool ok = score_lane && (base + ks * 8 + krow <= pos);
 #pragma unroll
-            for (int h = 0; h < G; h++) {
-                float d = 0.f;
+            for (int qd = 0; qd < GQ; qd++) {
+                f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int f = 0; f < NF; f++) d += dot4(qr[h][f], kb[ks][f]);
-                d = group_sum<LPR>(d);
-                s[ks][h] = (t <= pos) ? d : -INFINITY;
+                for (int f = 0; f < NF; f++) d = mfma4(qa[qd][f], kb[ks][f], d);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (4 * qd + i >= G) continue;
+                    const float v = slice_sum(d[i]);  // cross-lane: every lane takes part
+                    s[ks][4 * qd + i] = ok ? v : -INFINITY;
+                }
             }
         }
 
@@ -448,7 +465,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int h = 0; h < G; h++) {
-                const float m_new = fmaxf(m_ref[h], groups_max<LPR>(mt[h]));
+                const float m_new = fmaxf(m_ref[h], score_rows_max(mt[h]));
                 const float alpha = (m_ref[h] == -INFINITY) ? 0.0f : fast_exp2(m_ref[h] - m_new);
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[h / 4][e][h % 4] *= alpha;
@@ -461,19 +478,28 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 s[ks][h] = (s[ks][h] == -INFINITY) ? 0.0f : fast_exp2(s[ks][h] - m_ref[h]);
-                // every lane of a K row group holds the same p: l is kept per
-                // group here and summed across the groups once at the end
+                // the eight slice lanes of a row hold the same p: l is kept
+                // per lane and summed over the score rows once at the end
                 l_run[h] += s[ks][h];
             }
         }
 
-        // Probabilities to LDS, [row][head].
+        // Probabilities to LDS, [row][head], from one slice lane per row
+        // (lanes 16-19 and 48-51).
+        if ((lane & 0x1C) == 0x10) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            float pv = s[ks][0];
+            for (int ks = 0; ks < KS; ks++) {
+                float *dst = &p_lds[wave][(ks * 8 + krow) * G];
+                if constexpr (G % 4 == 0) {
 #pragma unroll
-            for (int h = 1; h < G; h++) pv = (kj == h) ? s[ks][h] : pv;
-            if (kj < G) p_lds[wave][(ks * RPK + kg) * G + kj] = pv;
+                    for (int qd = 0; qd < GQ; qd++)
+                        reinterpret_cast<float4 *>(dst)[qd] =
+                            make_float4(s[ks][4 * qd], s[ks][4 * qd + 1], s[ks][4 * qd + 2], s[ks][4 * qd + 3]);
+                } else {
+#pragma unroll
+                    for (int h = 0; h < G; h++) dst[h] = s[ks][h];
+                }
+            }
         }
         __builtin_amdgcn_wave_barrier();
 
@@ -504,7 +530,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
                                               acc[h / 4][2][h % 4], acc[h / 4][3][h % 4]);
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        const float lw = groups_sum<LPR>(l_run[h]);
+        const float lw = score_rows_sum(l_run[h]);
         if (lane == 0) {
             comb_l[wave][h] = lw;
             comb_m[wave][h] = m_ref[h];
@@ -548,44 +574,66 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // Fold records [first, first + n) of the G heads: thread = (head mh,
     // record lane mg, float4 column md4); record lane mg takes records
     // first + mg, first + mg + MG, ... with an online max, eight records of
-    // loads in flight at a time (L2 reads), then the record lanes meet in LDS.
+    // loads in flight at a time, then the record lanes meet in LDS.
     // Leaves (o, M, L) of head mh, columns md4, in the threads with mg == 0.
+    // The loads are device-scope (sc1), which always read L2: one 128-byte
+    // line holds the (max, sum) records of two sub-groups, and a copy that
+    // this CU's L1 took while folding one of them could predate the other's
+    // stores.
     const int mh = tid / (MG * D4), mg = (tid / D4) % MG, md4 = tid % D4;
     static_assert(sizeof(comb_o) >= sizeof(float4) * G * MG * D4, "merge scratch");
     static_assert(sizeof(p_lds) >= sizeof(float) * 2 * G * MG, "merge scratch");
     float4 *mo = &comb_o[0][0][0][0];      // [G][MG][D4]
     float *mmx = &p_lds[0][0];             // [G][MG]
     float *mls = &p_lds[0][0] + G * MG;    // [G][MG]
-    auto fold = [&](int first, int n, float4 &ox, float &Mx, float &Lx) {
-        constexpr int B = 8;
-        float mm = -INFINITY, ll = 0.f;
-        float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int c0 = mg; c0 < n; c0 += MG * B) {
+    constexpr int B = 8;  // records in flight per lane
+    // Online fold of records first + c, c = c_begin, c_begin + step, ... < n,
+    // into (oo, mm, ll): B records of loads in flight at a time (L2 reads).
+    auto fold_lane = [&](int first, int c_begin, int step, int n, float4 &oo, float &mm, float &ll) {
+        for (int c0 = c_begin; c0 < n; c0 += step * B) {
             float2 mlb[B];
             float4 ob[B];
 #pragma unroll
             for (int j = 0; j < B; j++) {
-                const int c = c0 + j * MG;
+                const int c = c0 + j * step;
                 const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
                 // past n: an offset at the end of the range reads 0
-                mlb[j] = buf_load2<kSc0>(wm_rsrc, c < n ? row * 8u : ws_ml_bytes);
-                ob[j] = buf_load4<kSc0>(wo_rsrc, c < n ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
+                mlb[j] = buf_load2<kSc1>(wm_rsrc, c < n ? row * 8u : ws_ml_bytes);
+                ob[j] = buf_load4<kSc1>(wo_rsrc, c < n ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
             }
             float m_new = mm;
 #pragma unroll
             for (int j = 0; j < B; j++)
-                if (c0 + j * MG < n) m_new = fmaxf(m_new, mlb[j].x);
+                if (c0 + j * step < n) m_new = fmaxf(m_new, mlb[j].x);
             const float al = (mm == -INFINITY) ? 0.f : fast_exp2(mm - m_new);
             scale4(oo, al);
             ll *= al;
 #pragma unroll
             for (int j = 0; j < B; j++) {
-                const float w = (c0 + j * MG < n) ? fast_exp2(mlb[j].x - m_new) : 0.f;
+                const float w = (c0 + j * step < n) ? fast_exp2(mlb[j].x - m_new) : 0.f;
                 fma4(oo, w, ob[j]);
                 ll += w * mlb[j].y;
             }
             mm = m_new;
         }
+    };
+    // Fold records [first, first + n) of the G heads into (ox, Mx, Lx) of
+    // the threads with mg == 0.  Up to B records are one batch of loads in
+    // those threads alone; more are spread over the MG record lanes, which
+    // then meet in LDS.
+    auto fold = [&](int first, int n, float4 &ox, float &Mx, float &Lx) {
+        if (n <= B) {
+            if (mg == 0) {
+                ox = make_float4(0.f, 0.f, 0.f, 0.f);
+                Mx = -INFINITY;
+                Lx = 0.f;
+                fold_lane(first, 0, 1, n, ox, Mx, Lx);
+            }
+            return;
+        }
+        float mm = -INFINITY, ll = 0.f;
+        float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
+        fold_lane(first, mg, MG, n, oo, mm, ll);
         __syncthreads();  // LDS scratch is free (combine buffers / earlier fold)
         mo[(mh * MG + mg) * D4 + md4] = oo;
         if (md4 == 0) {
@@ -619,12 +667,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        const int prev = __hip_atomic_fetch_add(ctr + 1 + sg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int prev = __hip_atomic_fetch_add(ctr + (1 + sg) * kCtrStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         s_last = (prev == sg_n - 1);
     }
     __syncthreads();
     if (!s_last) return;
-    if (tid == 0) ctr[1 + sg] = 0;
+    if (tid == 0) ctr[(1 + sg) * kCtrStride] = 0;
     float4 ox;
     float Mx, Lx;
     fold(sg * kSubGroup, sg_n, ox, Mx, Lx);
