@@ -188,11 +188,12 @@ def main():
                 att.step_async(l, pos, qp, kp, vp, op, sp)
     else:
         pp = pos_dev.data_ptr()
+        total_rows = int(np.sum(Ts))
 
         def one_step():
             for l in range(L):
                 qp, kp, vp, op = ptrs[l]
-                att.step_batched_async(l, batch, pp, max_pos, qp, kp, vp, op, sp)
+                att.step_batched_async(l, batch, pp, max_pos, qp, kp, vp, op, sp, total_rows)
 
     torch.cuda.synchronize()
     for _ in range(args.warmup):

@@ -99,11 +99,14 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
 /* As leap_hip_attention_step_batched with device pointers (pos included),
  * enqueued on `stream`.  max_pos is a host-side upper bound of pos[] used to
  * size the launch; sequences whose pos lies outside [0, max_pos] or beyond
- * seq_len are skipped and their outputs left unwritten. */
+ * seq_len are skipped and their outputs left unwritten.  total_rows is the
+ * host's sum of pos[i] + 1 when it has one (it only steers the split of the
+ * positions over workgroups), or 0 when it does not: the launch is then
+ * sized as if the sequences were spread evenly up to max_pos. */
 int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int n_seq,
-                                          const int *pos, int max_pos, const float *q,
-                                          const float *k_new, const float *v_new, float *out,
-                                          void *stream);
+                                          const int *pos, int max_pos, long long total_rows,
+                                          const float *q, const float *k_new, const float *v_new,
+                                          float *out, void *stream);
 
 /* clear_kv_cache (FloatTransformer.cpp:74-77): zero both caches. */
 int leap_hip_attention_clear(leap_hip_attention *h);

@@ -67,7 +67,8 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_step.argtypes = [H, _I, _I, _F, _F, _F, _F]
     L.leap_hip_attention_step_async.argtypes = [H, _I, _I, _P, _P, _P, _P, _P]
     L.leap_hip_attention_step_batched.argtypes = [H, _I, _I, ctypes.POINTER(_I), _F, _F, _F, _F]
-    L.leap_hip_attention_step_batched_async.argtypes = [H, _I, _I, _P, _I, _P, _P, _P, _P, _P]
+    L.leap_hip_attention_step_batched_async.argtypes = [H, _I, _I, _P, _I, ctypes.c_longlong, _P, _P,
+                                                        _P, _P, _P]
     L.leap_hip_attention_clear.argtypes = [H]
     L.leap_hip_attention_kv_upload.argtypes = [H, _I, _I, _I, _I, _F, _F]
     L.leap_hip_attention_kv_download.argtypes = [H, _I, _I, _I, _I, _F, _F]
@@ -161,9 +162,11 @@ class HipAttention:
         return out.reshape(n, self.q_dim)
 
     def step_batched_async(self, layer, n_seq, pos_ptr, max_pos, q_ptr, k_ptr, v_ptr, out_ptr,
-                           stream=0):
+                           stream=0, total_rows=0):
+        """total_rows: sum of pos[i] + 1 if known on the host (sizes the split), else 0."""
         self._check(self.lib.leap_hip_attention_step_batched_async(
-            self.h, layer, n_seq, pos_ptr, max_pos, q_ptr, k_ptr, v_ptr, out_ptr, stream))
+            self.h, layer, n_seq, pos_ptr, max_pos, total_rows, q_ptr, k_ptr, v_ptr, out_ptr,
+            stream))
 
     # -- cache management ---------------------------------------------------
     def clear(self):

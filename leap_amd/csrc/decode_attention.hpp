@@ -47,9 +47,9 @@ constexpr int kCounters = (1 + kMaxSub) * kCtrStride;  // counter words per (seq
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 
-// Rows of one wave sub-tile: 16 KiB of K and V (8 KiB each), whatever the
-// number of q heads per KV head.
-__host__ __device__ constexpr int subtile_rows(int hd, int g) { return (void)g, 2048 / hd; }
+// Rows of one wave sub-tile: 16 (two MFMA row sets), i.e. 16 KiB of K and V
+// at head_dim 128, whatever the number of q heads per KV head.
+__host__ __device__ constexpr int subtile_rows(int hd, int g) { return (void)hd, (void)g, 16; }
 
 // Positions one workgroup pass covers with NW waves; chunk sizes are
 // multiples of it.
@@ -317,7 +317,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // folded in, and shared through LDS; only the workgroup whose chunk holds
     // pos loads and rotates the new token's k and v.
     const int chunk_begin = chunk_id * a.chunk;
-    const int n_sub = a.chunk / S::ROWS;
+    // passes over this chunk's rows that reach a position <= pos
+    const int n_sub = (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
     const bool has_pos = (chunk_id == n_chunks - 1);
     constexpr int PAIRS = G * HD / 2;
     constexpr int QP = (PAIRS + S::THREADS - 1) / S::THREADS;  // q pairs per thread

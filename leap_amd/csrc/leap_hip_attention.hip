@@ -38,6 +38,7 @@ struct leap_hip_attention {
     float *q_dev = nullptr, *k_dev = nullptr, *v_dev = nullptr, *out_dev = nullptr;
     hipStream_t stream = nullptr;
     int split = 0;
+    int n_cu = 256;  // compute units of the device
     std::string err;
 };
 
@@ -93,10 +94,19 @@ int check_layer(leap_hip_attention *h, int layer)
 
 int round_up(int x, int q) { return (x + q - 1) / q * q; }
 
-// Positions per workgroup: enough workgroups to keep every CU streaming
-// (about 1024 over the launch), at least one quantum, and at most kMaxChunks
-// chunks per sequence.
-int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
+// Positions per workgroup (chunk), from the size and shape of the launch:
+//   - small launches (K/V bytes up to kLatencyBytes) are latency-bound: two
+//     workgroups per CU, all resident at once, each one pass of its waves;
+//   - large launches of equal-length sequences stream best with one
+//     workgroup per CU walking a long contiguous run of rows;
+//   - large ragged batches (mean length under 3/4 of the longest) take
+//     about 12 workgroups per CU over the launch, so that the last ones to
+//     start are short.
+// The sequence length (the mean one when ragged) is cut into equal chunks,
+// rounded up to whole passes; at most kMaxChunks chunks per sequence.
+constexpr long long kLatencyBytes = 128ll << 20;
+
+int choose_chunk(const leap_hip_attention *h, int n_seq, long long total_rows, int max_T)
 {
     const int quantum = leap::rows_per_pass(h->cfg.head_dim, h->group, kWaves);
     const int floor_chunk = round_up((max_T + leap::kMaxChunks - 1) / leap::kMaxChunks, quantum);
@@ -104,10 +114,14 @@ int choose_chunk(const leap_hip_attention *h, long long total_rows, int max_T)
     if (h->split > 0) {
         c = round_up(h->split, quantum);
     } else {
-        const long long target_wgs = 1024;
-        long long per = (total_rows * h->cfg.n_kv_heads + target_wgs - 1) / target_wgs;
-        per = std::min<long long>(per, 1 << 20);
-        c = round_up((int)per, quantum);
+        const long long bytes = total_rows * h->kv_dim * 8ll;
+        const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
+        const long long per_cu = bytes <= kLatencyBytes ? 2 : ragged ? 12 : 1;
+        const long long n_groups = (long long)n_seq * h->cfg.n_kv_heads;
+        const long long want_wgs = std::max<long long>(1, per_cu * h->n_cu);
+        const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
+        const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
+        c = round_up((int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20), quantum);
     }
     c = std::min(c, round_up(max_T, quantum));
     return std::max(c, std::max(floor_chunk, quantum));
@@ -120,7 +134,7 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     const int hd = h->cfg.head_dim;
     KernelFn fn = pick_kernel(hd, h->group);
     if (!fn) return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", hd, h->group);
-    const int chunk = choose_chunk(h, total_rows, max_pos + 1);
+    const int chunk = choose_chunk(h, n_seq, total_rows, max_pos + 1);
     const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
 
     leap::StepArgs a{};
@@ -218,6 +232,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     } while (0)
 
     CREATE_TRY(hipSetDevice(c.device));
+    CREATE_TRY(hipDeviceGetAttribute(&h->n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
     CREATE_TRY(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     const size_t cache_bytes = (size_t)c.max_batch * h->slab_floats * sizeof(float);
     CREATE_TRY(hipMalloc(&h->k_cache, cache_bytes));
@@ -307,9 +322,9 @@ int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const flo
 }
 
 int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int n_seq,
-                                          const int *pos, int max_pos, const float *q,
-                                          const float *k_new, const float *v_new, float *out,
-                                          void *stream)
+                                          const int *pos, int max_pos, long long total_rows,
+                                          const float *q, const float *k_new, const float *v_new,
+                                          float *out, void *stream)
 {
     if (!h) return -EINVAL;
     if (int rc = check_layer(h, layer)) return rc;
@@ -319,9 +334,12 @@ int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int 
         return set_err(h, -EINVAL, "max_pos %d outside [0, %d)", max_pos, h->cfg.seq_len);
     if (!pos || !q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
-    // Without the host positions, size the chunks as if every sequence were
-    // half the longest.
-    const long long rows = (long long)n_seq * (max_pos + 1) / 2 + 1;
+    if (total_rows < 0 || total_rows > (long long)n_seq * (max_pos + 1))
+        return set_err(h, -EINVAL, "total_rows %lld outside [0, %lld]", total_rows,
+                       (long long)n_seq * (max_pos + 1));
+    // Without the host's row count, size the chunks as if the lengths were
+    // spread evenly up to the longest.
+    const long long rows = total_rows > 0 ? total_rows : (long long)n_seq * (max_pos + 1) / 2 + 1;
     return launch(h, layer, n_seq, pos, 0, max_pos, rows, q, k_new, v_new, out,
                   (hipStream_t)stream);
 }

@@ -275,3 +275,13 @@ def test_async_entry_points_on_a_torch_stream():
         s.synchronize()
         assert np.array_equal(bout[0].cpu().numpy(), ref)
         _step_and_check(att, 0, 17, q, k, v, 500000.0, seq=1, out=bout[1].cpu().numpy())
+        # the host's row count only changes how the positions are split
+        hint = torch.empty_like(bout)
+        att.step_batched_async(0, 2, pos.data_ptr(), T - 1, bq.data_ptr(), bk.data_ptr(),
+                               bv.data_ptr(), hint.data_ptr(), s.cuda_stream, total_rows=T + 18)
+        s.synchronize()
+        assert_close(hint[0].cpu().numpy(), ref)
+        assert_close(hint[1].cpu().numpy(), bout[1].cpu().numpy())
+        with pytest.raises(LeapError):
+            att.step_batched_async(0, 2, pos.data_ptr(), T - 1, bq.data_ptr(), bk.data_ptr(),
+                                   bv.data_ptr(), hint.data_ptr(), s.cuda_stream, total_rows=2 * T + 1)
