@@ -332,20 +332,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             qt[i] = rope2[pair % (HD / 2)];
         }
     }
-    float4 tab[NF], knew[NF];
-    float4 vnew = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (has_pos) {
-#pragma unroll
-        for (int f = 0; f < NF; f++) {
-            const int d4 = 8 * f + ksl;
-            tab[f] = rope_row[d4];
-            knew[f] = *reinterpret_cast<const float4 *>(k_row_new + 4 * d4);
-        }
-        vnew = *reinterpret_cast<const float4 *>(v_row_new + 4 * vj);
-    }
-
     float4 kb[KS][NF], vb[VS];
-    auto load_tile = [&](int sub) {
+    auto load_k = [&](int sub) {
         const int base = chunk_begin + (sub * NW + wave) * R;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
@@ -354,32 +342,54 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             for (int f = 0; f < NF; f++)
                 kb[ks][f] = buf_load4(k_rsrc, roff + 16u * (uint32_t)(8 * f + ksl));
         }
+    };
+    auto load_v = [&](int sub) {
+        const int base = chunk_begin + (sub * NW + wave) * R;
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const uint32_t roff = (uint32_t)(base + vs * RPV + vg) * row_bytes;
             vb[vs] = buf_load4(v_rsrc, roff + 16u * (uint32_t)vj);
         }
     };
-
-    load_tile(0);
-
     // q: rotate (fused multiply-adds are fine, q is not stored) and scale so
-    // scores come out in log2 units; k: exactly as the reference rotates it,
-    // since it is stored.
+    // scores come out in log2 units.
     float *q_flat = reinterpret_cast<float *>(&q_lds[0][0]);
+    auto rotate_q = [&]() {
 #pragma unroll
-    for (int i = 0; i < QP; i++) {
-        const int pair = tid + i * S::THREADS;
-        if (pair < PAIRS) {
-            const float x0 = qp[i].x, x1 = qp[i].y, c = qt[i].x, sn = qt[i].y;
-            q_flat[2 * pair] = (x0 * c - x1 * sn) * a.scale_log2;
-            q_flat[2 * pair + 1] = (x1 * c + x0 * sn) * a.scale_log2;
+        for (int i = 0; i < QP; i++) {
+            const int pair = tid + i * S::THREADS;
+            if (pair < PAIRS) {
+                const float x0 = qp[i].x, x1 = qp[i].y, c = qt[i].x, sn = qt[i].y;
+                q_flat[2 * pair] = (x0 * c - x1 * sn) * a.scale_log2;
+                q_flat[2 * pair + 1] = (x1 * c + x0 * sn) * a.scale_log2;
+            }
         }
-    }
-    if (has_pos) {
+    };
+
+    // First tile, in the order q (above), K rows, the new token's k and its
+    // table entries, V rows, the new token's v.  Every workgroup issues the
+    // new token's loads, through descriptors that are empty outside the
+    // workgroup holding pos (those loads return 0 without touching memory):
+    // without a branch, the waits (which count outstanding loads in issue
+    // order) stay exact, and the prologue barrier waits for q alone.
+    const uint32_t new_bytes = has_pos ? (uint32_t)HD * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t tab_rsrc = make_rsrc(rope_row, new_bytes);
+    const __amdgpu_buffer_rsrc_t kn_rsrc = make_rsrc(k_row_new, new_bytes);
+    const __amdgpu_buffer_rsrc_t vn_rsrc = make_rsrc(v_row_new, new_bytes);
+    // (scheduling barriers keep the compiler from reordering the groups)
+    float4 tab[NF], knew[NF];
+    load_k(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int f = 0; f < NF; f++) knew[f] = rope4(knew[f], tab[f]);
+    for (int f = 0; f < NF; f++) {
+        tab[f] = buf_load4(tab_rsrc, 16u * (uint32_t)(8 * f + ksl));
+        knew[f] = buf_load4(kn_rsrc, 16u * (uint32_t)(8 * f + ksl));
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(0);
+    const float4 vnew = buf_load4(vn_rsrc, 16u * (uint32_t)vj);
+    __builtin_amdgcn_sched_barrier(0);
+    rotate_q();
     __syncthreads();
     // Score MFMA A operand: head 4*quad + kj at this lane's dims (zero for
     // the unused heads of a partial quad).
@@ -406,28 +416,28 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         for (int e = 0; e < 4; e++) acc[q][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int sub = 0; sub < n_sub; sub++) {
-        if (sub > 0) load_tile(sub);
+        if (sub > 0) {
+            load_k(sub);
+            load_v(sub);
+        }
         const int base = chunk_begin + (sub * NW + wave) * R;
 
-        // The new token's row: the rotated k_new / v_new replace the (zero)
-        // loads, and are appended to cache[layer][pos].
+        // The new token's row: k_new, rotated exactly as the reference
+        // rotates it (it is stored), and v_new are appended to
+        // cache[layer][pos] and replace the (zero) loads of that row, k here
+        // (the scores wait for the K loads anyway) and v just before the
+        // weighted V (it is loaded last): overwriting a register whose load
+        // is still in flight, or storing a loaded value, first waits for
+        // that load.
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const int t = base + ks * 8 + krow;
             if (t == pos) {
 #pragma unroll
                 for (int f = 0; f < NF; f++) {
-                    kb[ks][f] = knew[f];
-                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = knew[f];
+                    kb[ks][f] = rope4(knew[f], tab[f]);
+                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = kb[ks][f];
                 }
-            }
-        }
-#pragma unroll
-        for (int vs = 0; vs < VS; vs++) {
-            const int t = base + vs * RPV + vg;
-            if (t == pos) {
-                vb[vs] = vnew;
-                *reinterpret_cast<float4 *>(vc + (size_t)t * kv_dim + 4 * vj) = vnew;
             }
         }
 
@@ -511,6 +521,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const int r = vs * RPV + vg;
+            if (base + r == pos) {
+                vb[vs] = vnew;
+                *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
+            }
 #pragma unroll
             for (int q = 0; q < GQ; q++) {
                 const int h = 4 * q + (lane & 3);
