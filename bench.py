@@ -17,6 +17,13 @@ The CPU baseline is the oracle (the restated reference attention, OpenMP over
 heads, AVX2) timed on the host cores on a bounded sample of the same workload:
 the same device bytes of a few layers of sequence 0, downloaded.
 
+The `*-block-*` workloads time the whole attention sub-block of the layer step
+instead (rmsnorm, q/k/v projections, attention, wo projection and residual;
+three launches per layer-step), with synthetic N(0,1)/sqrt(dim) weights: one
+random set uploaded into every layer's own slot, so each layer streams its own
+copy from HBM.  Their bytes add the weights (Wq, Wk, Wv, Wo, rms) and the
+residual stream to B(T).
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
 """
 from __future__ import annotations
@@ -36,6 +43,8 @@ sys.path.insert(0, ROOT)
 METRIC = "attn decode µs/layer-step + HBM GB/s (% of peak), Llama-3-8B shape ctx 4096"
 HBM_PEAK_GBS = 8000.0
 KERNEL = "decode_attention_kernel"
+BLOCK_METRIC = "attn sub-block (rmsnorm, qkv, attention, wo, residual) µs/layer-step + HBM GB/s, Llama-3-8B ctx 4096"
+BLOCK_KERNELS = "qkv_kernel + decode_attention_kernel + proj_residual_kernel"
 SEED = 0x4C454150
 
 # name -> (layers, n_heads, n_kv_heads, head_dim, theta, batch, context, seed index)
@@ -46,10 +55,12 @@ WORKLOADS = {
     "llama3-8b-batch64-ragged": (32, 32, 8, 128, 500000.0, 64, ("ragged", 512, 8192), 2),
     "llama3-70b-stage20-batch16": (20, 64, 8, 128, 500000.0, 16, 8192, 3),
     "llama3.1-8b-ctx131072": (32, 32, 8, 128, 500000.0, 1, 131072, 4),
+    "llama3-8b-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 5),
 }
+BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096"}
 DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3-8b-batch64-ragged": 10, "llama3-70b-stage20-batch16": 10,
-                 "llama3.1-8b-ctx131072": 10}
+                 "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30}
 
 
 def algorithmic_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
@@ -58,6 +69,14 @@ def algorithmic_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
     RoPE table row."""
     kv_dim, dim = n_kv * hd, n_heads * hd
     return 8 * T * kv_dim + 8 * dim + 16 * kv_dim + 4 * hd
+
+
+def block_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
+    """Bytes of one attention sub-block layer-step: the attention's B(T), the
+    weights Wq, Wk, Wv, Wo and rms_att, and the residual stream read twice and
+    written once."""
+    dim, kv_dim = n_heads * hd, n_kv * hd
+    return algorithmic_bytes(T, n_heads, n_kv, hd) + 4 * ((dim + 2 * kv_dim) * dim + dim * dim + dim) + 12 * dim
 
 
 def traffic_from_profiles(workload: str):
@@ -76,6 +95,43 @@ def contexts(workload: str):
         rng = np.random.default_rng(SEED + sidx)
         return rng.integers(ctx[1], ctx[2] + 1, size=batch).astype(np.int64)
     return np.full(batch, ctx, np.int64)
+
+
+def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights):
+    """The oracle's sub-block chain (rmsnorm, matmul, attention, matmul,
+    residual), OpenMP over rows and heads, on the host, on layers
+    [0, n_layers_sample) with the device cache bytes downloaded."""
+    from oracle import oracle as O
+    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    if not os.path.isfile(O.ORACLE_SO):
+        O.build(ref=False)
+    env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(env_threads or os.cpu_count() or 1, 16)
+    O.lib().oracle_set_threads(threads)
+    T = int(Ts[0])
+    n_l = min(n_layers_sample, L)
+    orc = O.Oracle(n_l, nh, nkv, hd, T, theta=theta)
+    for l in range(n_l):
+        k, v = att.kv_download(0, l, 0, T)
+        orc.key_cache[l] = k
+        orc.value_cache[l] = v
+    x = np.random.default_rng(SEED + sidx).standard_normal(nh * hd).astype(np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        for l in range(n_l):
+            orc.block(l, T - 1, x, *weights)
+        times.append((time.perf_counter() - t0) / n_l)
+    us = float(np.median(times)) * 1e6
+    gbs = block_bytes(T, nh, nkv, hd) / (us * 1e-6) / 1e9
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "us_per_layer_step": round(us, 2),
+        "sample": f"{len(times)} sweeps of the sub-block over layers 0..{n_l - 1} of the same workload "
+                  f"(context {T}), device cache bytes downloaded; median per layer-step; OpenMP over "
+                  f"rows and heads",
+    }
 
 
 def cpu_baseline(att, workload, Ts, n_layers_sample: int, budget_s: float):
@@ -179,7 +235,28 @@ def main():
     sp = stream.cuda_stream
     ptrs = [(q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(), out[l].data_ptr()) for l in range(L)]
 
-    if batch == 1:
+    is_block = args.workload in BLOCK_WORKLOADS
+    weights = None
+    if is_block:
+        dim, kvd = nh * hd, nkv * hd
+        wrng = np.random.default_rng(SEED + sidx)
+        weights = (
+            (1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32),
+            (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
+            (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
+            (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
+            (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
+        )
+        for l in range(L):
+            att.set_layer_weights(l, *weights)
+        x_res = torch.randn(dim, device=dev, generator=g)
+        xp = x_res.data_ptr()
+        pos = int(Ts[0]) - 1
+
+        def one_step():
+            for l in range(L):
+                att.block_async(l, pos, xp, sp)
+    elif batch == 1:
         pos = int(Ts[0]) - 1
 
         def one_step():
@@ -214,14 +291,15 @@ def main():
 
     launches = steps * L
     us_layer = ms_total * 1e3 / launches
-    bytes_layer = int(sum(algorithmic_bytes(int(T), nh, nkv, hd) for T in Ts))
+    per_seq = block_bytes if is_block else algorithmic_bytes
+    bytes_layer = int(sum(per_seq(int(T), nh, nkv, hd) for T in Ts))
     gbs = bytes_layer / (us_layer * 1e-6) / 1e9
-    if not np.isfinite(out.float().sum().item()):
-        print("non-finite attention output", file=sys.stderr)
+    if not np.isfinite((x_res if is_block else out).float().sum().item()):
+        print("non-finite output", file=sys.stderr)
         sys.exit(1)
 
     result = {
-        "metric": METRIC,
+        "metric": BLOCK_METRIC if is_block else METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -232,7 +310,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache and q/k/v, generated on the device)",
+        "data": (f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache generated on the device; "
+                 f"N(0,1)/sqrt(dim) weights, one set uploaded into every layer)") if is_block else
+                f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache and q/k/v, generated on the device)",
         "config": {
             "workload": args.workload, "n_layers": L, "n_heads": nh, "n_kv_heads": nkv,
             "head_dim": hd, "batch": batch, "rope_theta": theta,
@@ -244,7 +324,7 @@ def main():
         "tokens_layers_per_s": round(batch * 1e6 / us_layer, 1),
         "host_wall_s": round(wall, 4),
         "roofline": {
-            "kernel": KERNEL,
+            "kernel": BLOCK_KERNELS if is_block else KERNEL,
             "bound": "hbm",
             "achieved": round(gbs, 2),
             "peak": HBM_PEAK_GBS,
@@ -258,8 +338,12 @@ def main():
     }
     if not args.no_cpu:
         try:
-            result["cpu_baseline"] = cpu_baseline(att, args.workload, Ts, args.cpu_layers,
-                                                  args.cpu_seconds)
+            if is_block:
+                result["cpu_baseline"] = cpu_baseline_block(att, args.workload, Ts, args.cpu_layers,
+                                                            args.cpu_seconds, weights)
+            else:
+                result["cpu_baseline"] = cpu_baseline(att, args.workload, Ts, args.cpu_layers,
+                                                      args.cpu_seconds)
         except Exception as e:  # the GPU line still stands; say why the CPU leg is missing
             result["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
     att.close()

@@ -120,6 +120,32 @@ int leap_hip_attention_kv_upload(leap_hip_attention *h, int seq, int layer, int 
 int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, int pos_begin,
                                    int pos_end, float *k, float *v);
 
+/* ---- The attention sub-block of run_layer on the device ----------------- */
+
+/* Weights of one held layer for leap_hip_attention_block, copied from host
+ * memory in the reference's layout (FloatTransformerWeights,
+ * FloatTransformer.h:9-22; the layer's slices start at l*dim, l*dim*dim and
+ * l*dim*kv_dim as run_layer reads them, FloatTransformer.cpp:394-402, 664):
+ * rms_att [dim], wq [dim][dim], wk [kv_dim][dim], wv [kv_dim][dim],
+ * wo [dim][dim], row-major, dim = n_heads * head_dim.  The projections need
+ * dim in {2048, 4096, 8192}; other sizes return -EINVAL.  Device memory for
+ * every held layer is allocated on the first call. */
+int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const float *rms_att,
+                                         const float *wq, const float *wk, const float *wv,
+                                         const float *wo);
+
+/* run_layer from its start to the attention residual
+ * (FloatTransformer.cpp:394-683): xb = rmsnorm(x, rms_att) (:394, rmsnorm
+ * :88-213), q, k, v = Wq, Wk, Wv . xb (:400-402, matmul :240-382), the
+ * attention block of leap_hip_attention_step (k and v appended to
+ * cache[layer][pos]), then x += Wo . out (:664-683).  x is the dim-float
+ * residual stream, updated in place: a device pointer, enqueued on `stream`. */
+int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, float *x,
+                                   void *stream);
+
+/* As leap_hip_attention_block_async with a host pointer, synchronous. */
+int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x);
+
 /* ---- Extras with no counterpart in the reference ---------------------- */
 
 /* Fill every cache row of every held sequence and layer with seeded

@@ -30,6 +30,8 @@ EXPORTS = (
     "leap_hip_attention_clear", "leap_hip_attention_kv_upload", "leap_hip_attention_kv_download",
     "leap_hip_attention_kv_fill_normal", "leap_hip_attention_rope_download",
     "leap_hip_attention_set_split", "leap_hip_attention_kv_device_ptr",
+    "leap_hip_attention_set_layer_weights", "leap_hip_attention_block",
+    "leap_hip_attention_block_async",
 )
 
 
@@ -77,6 +79,9 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_set_split.argtypes = [H, _I]
     L.leap_hip_attention_kv_device_ptr.argtypes = [H, _I, _I, ctypes.POINTER(_P),
                                                    ctypes.POINTER(_P)]
+    L.leap_hip_attention_set_layer_weights.argtypes = [H, _I, _F, _F, _F, _F, _F]
+    L.leap_hip_attention_block.argtypes = [H, _I, _I, _F]
+    L.leap_hip_attention_block_async.argtypes = [H, _I, _I, _P, _P]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -167,6 +172,22 @@ class HipAttention:
         self._check(self.lib.leap_hip_attention_step_batched_async(
             self.h, layer, n_seq, pos_ptr, max_pos, total_rows, q_ptr, k_ptr, v_ptr, out_ptr,
             stream))
+
+    # -- the attention sub-block (rmsnorm, q/k/v, attention, wo, residual) ---
+    def set_layer_weights(self, layer, rms_att, wq, wk, wv, wo):
+        """Upload one layer's weights, row-major as the reference holds them."""
+        d, kv = self.q_dim, self.kv_dim
+        arrs = (_f32(rms_att, d), _f32(wq, d * d), _f32(wk, kv * d), _f32(wv, kv * d), _f32(wo, d * d))
+        self._check(self.lib.leap_hip_attention_set_layer_weights(self.h, layer, *(_fp(a) for a in arrs)))
+
+    def block(self, layer, pos, x):
+        """x + Wo . attention(Wq/Wk/Wv . rmsnorm(x)); returns the new residual stream."""
+        x = _f32(x, self.q_dim).copy()
+        self._check(self.lib.leap_hip_attention_block(self.h, layer, pos, _fp(x)))
+        return x
+
+    def block_async(self, layer, pos, x_ptr, stream=0):
+        self._check(self.lib.leap_hip_attention_block_async(self.h, layer, pos, x_ptr, stream))
 
     # -- cache management ---------------------------------------------------
     def clear(self):

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "decode_attention.hpp"
+#include "gemv.hpp"
 
 extern "C" void leap_rope_table_host(int seq_len, int head_size, float theta, float *cos_tab,
                                      float *sin_tab);
@@ -36,6 +37,13 @@ struct leap_hip_attention {
     int *counters = nullptr;
     int *pos_dev = nullptr;
     float *q_dev = nullptr, *k_dev = nullptr, *v_dev = nullptr, *out_dev = nullptr;
+    // attention sub-block: per-layer weights (allocated on the first
+    // set_layer_weights) and the block's own q, k, v, attention-out buffers
+    float *w_qkv = nullptr;   // [n_local][dim + 2*kv_dim][dim]
+    float *w_o = nullptr;     // [n_local][dim][dim]
+    float *w_rms = nullptr;   // [n_local][dim]
+    std::vector<char> w_set;  // per held layer: weights uploaded
+    float *blk = nullptr;     // q [dim] | k [kv_dim] | v [kv_dim] | xb [dim] | x staging [dim]
     hipStream_t stream = nullptr;
     int split = 0;
     int n_cu = 256;  // compute units of the device
@@ -171,6 +179,60 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     return 0;
 }
 
+// Projection kernels by dim = 1024 * NC; RB rows per workgroup keep 64 KiB of
+// weights in flight per workgroup.
+using QkvFn = void (*)(leap::QkvArgs);
+using ProjFn = void (*)(leap::ProjArgs);
+template <int NC>
+constexpr int proj_rows() { return 16 / NC; }
+
+bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
+{
+#define LEAP_PROJ(NC)                                                             \
+    if (dim == 1024 * NC) {                                                       \
+        *qkv = leap::qkv_kernel<proj_rows<NC>(), NC>;                             \
+        *proj = leap::proj_residual_kernel<proj_rows<NC>(), NC>;                  \
+        *rb = proj_rows<NC>();                                                    \
+        return true;                                                              \
+    }
+    LEAP_PROJ(2) LEAP_PROJ(4) LEAP_PROJ(8)
+#undef LEAP_PROJ
+    return false;
+}
+
+int launch_block(leap_hip_attention *h, int layer, int pos, float *x, hipStream_t stream)
+{
+    QkvFn qkv;
+    ProjFn proj;
+    int rb;
+    const int dim = h->q_dim, kv = h->kv_dim;
+    if (!pick_proj(dim, &qkv, &proj, &rb))
+        return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
+    const int li = layer - h->cfg.layer_begin;
+    if (!h->w_qkv || !h->w_set[li]) return set_err(h, -EINVAL, "no weights set for layer %d", layer);
+    float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
+    leap::QkvArgs qa{};
+    qa.x = x;
+    qa.rms_w = h->w_rms + (size_t)li * dim;
+    qa.w = h->w_qkv + (size_t)li * (dim + 2 * kv) * dim;
+    qa.q = q;
+    qa.k = k;
+    qa.v = v;
+    qa.dim = dim;
+    qa.kv_dim = kv;
+    hipLaunchKernelGGL(qkv, dim3((unsigned)((dim + 2 * kv + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, qa);
+    HIP_TRY(h, hipGetLastError());
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
+    leap::ProjArgs pa{};
+    pa.xb = xb;
+    pa.w = h->w_o + (size_t)li * dim * dim;
+    pa.x = x;
+    pa.d = dim;
+    hipLaunchKernelGGL(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, pa);
+    HIP_TRY(h, hipGetLastError());
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -263,6 +325,8 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMalloc(&h->out_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->k_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->v_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->blk, (size_t)(3 * h->q_dim + 2 * h->kv_dim) * sizeof(float)));
+    h->w_set.assign(h->n_local, 0);
     CREATE_TRY(hipStreamSynchronize(h->stream));
 #undef CREATE_TRY
     *out = h;
@@ -273,7 +337,9 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
 {
     if (!h) return 0;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
-    void *bufs[] = {h->k_cache, h->v_cache, h->rope, h->ws_o, h->ws_ml, h->counters, h->pos_dev, h->q_dev, h->k_dev, h->v_dev, h->out_dev};
+    void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->pos_dev,
+                    h->q_dev,   h->k_dev,   h->v_dev, h->out_dev, h->blk,  h->w_qkv,    h->w_o,
+                    h->w_rms};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -375,6 +441,70 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
         return rc;
     HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, (size_t)n_seq * h->q_dim * sizeof(float),
                               hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    return 0;
+}
+
+int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const float *rms_att,
+                                         const float *wq, const float *wk, const float *wv,
+                                         const float *wo)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (!rms_att || !wq || !wk || !wv || !wo) return set_err(h, -EINVAL, "NULL weight");
+    QkvFn qkv;
+    ProjFn proj;
+    int rb;
+    const int dim = h->q_dim, kv = h->kv_dim;
+    if (!pick_proj(dim, &qkv, &proj, &rb))
+        return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    const size_t n_qkv = (size_t)(dim + 2 * kv) * dim, n_o = (size_t)dim * dim;
+    if (!h->w_qkv) {
+        HIP_TRY(h, hipMalloc(&h->w_qkv, (size_t)h->n_local * n_qkv * sizeof(float)));
+        HIP_TRY(h, hipMalloc(&h->w_o, (size_t)h->n_local * n_o * sizeof(float)));
+        HIP_TRY(h, hipMalloc(&h->w_rms, (size_t)h->n_local * dim * sizeof(float)));
+    }
+    const int li = layer - h->cfg.layer_begin;
+    float *dq = h->w_qkv + (size_t)li * n_qkv;
+    hipStream_t s = h->stream;
+    HIP_TRY(h, hipMemcpyAsync(dq, wq, (size_t)dim * dim * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(dq + (size_t)dim * dim, wk, (size_t)kv * dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(dq + (size_t)(dim + kv) * dim, wv, (size_t)kv * dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->w_o + (size_t)li * n_o, wo, n_o * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->w_rms + (size_t)li * dim, rms_att, (size_t)dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    h->w_set[li] = 1;
+    return 0;
+}
+
+int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, float *x, void *stream)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (pos < 0 || pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
+    if (!x) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    return launch_block(h, layer, pos, x, (hipStream_t)stream);
+}
+
+int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (pos < 0 || pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
+    if (!x) return set_err(h, -EINVAL, "NULL buffer");
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    hipStream_t s = h->stream;
+    float *xd = h->blk + 2 * h->q_dim + 2 * h->kv_dim;
+    HIP_TRY(h, hipMemcpyAsync(xd, x, (size_t)h->q_dim * sizeof(float), hipMemcpyHostToDevice, s));
+    if (int rc = launch_block(h, layer, pos, xd, s)) return rc;
+    HIP_TRY(h, hipMemcpyAsync(x, xd, (size_t)h->q_dim * sizeof(float), hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
     return 0;
 }

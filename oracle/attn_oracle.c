@@ -28,6 +28,12 @@
  *   oracle_rope_table     bitwise against the reference's own table
  *                         (oracle/_ref harness), cos=1/sin=0 at pos 0,
  *                         freq_0 = 1, cos^2+sin^2 = 1.
+ *   oracle_rmsnorm,       bitwise against the reference's own rmsnorm and
+ *   oracle_matmul         matmul (oracle/_ref harness, committed golden
+ *                         fixtures); closed forms: a constant vector
+ *                         normalises to w / sqrt(1 + 1e-5/c^2) * sign, an
+ *                         identity matrix returns x, a one-hot x returns a
+ *                         column of W, linearity in x.
  *   oracle_attention_step against the reference's run_layer (oracle/_ref
  *                         harness, committed golden fixtures), float64
  *                         brute force on tiny shapes, and closed forms
@@ -35,6 +41,7 @@
  *                         dominant key returns its value row, position
  *                         permutation invariance, pos 0 RoPE identity).
  */
+#include <immintrin.h>
 #include <math.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -95,23 +102,63 @@ static inline float hsum8(v8f v)
     return (b0 + b1) + (b2 + b3);
 }
 
-/* q.k with eight lane accumulators and the reference's horizontal sum, then
- * the scalar tail for head sizes that are not a multiple of 8
- * (FloatTransformer.cpp:516-630). */
+/* a.b with one chain of eight-lane fused multiply-adds and the reference's
+ * horizontal sum, then the scalar tail for lengths that are not a multiple of
+ * 8 (the q.k dots of FloatTransformer.cpp:516-630 and every row of matmul,
+ * :240-382).  Written with the reference's own intrinsics: a generic-vector
+ * accumulator would let -ffast-math -funroll-loops split the chain into
+ * several partial sums, which changes the rounding. */
 static inline float dot_ref(const float *q, const float *k, int n)
 {
-    v8f acc = {0, 0, 0, 0, 0, 0, 0, 0};
+    __m256 acc = _mm256_setzero_ps();
     int i = 0;
-    for (; i <= n - 8; i += 8) {
-        v8f qv, kv;
-        memcpy(&qv, q + i, sizeof qv);
-        memcpy(&kv, k + i, sizeof kv);
-        acc = qv * kv + acc;
-    }
-    float s = hsum8(acc);
+    for (; i <= n - 8; i += 8)
+        acc = _mm256_fmadd_ps(_mm256_loadu_ps(q + i), _mm256_loadu_ps(k + i), acc);
+    __m128 lo = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+    lo = _mm_hadd_ps(lo, lo);
+    lo = _mm_hadd_ps(lo, lo);
+    float s = _mm_cvtss_f32(lo);
     for (; i < n; i++)
         s += q[i] * k[i];
     return s;
+}
+
+/* FloatTransformer.cpp:79-213 (the AVX2 path): ss = sum of x^2 with eight
+ * lane FMA accumulators and the reference's horizontal sum, then the scalar
+ * tail; ss = ss / size + 1e-5; the hardware reciprocal-square-root estimate
+ * refined by one Newton step, (0.5 * est) * (3 - ss * est^2); o = w * (ss * x). */
+void oracle_rmsnorm(float *o, const float *x, const float *w, int size)
+{
+    v8f acc = {0, 0, 0, 0, 0, 0, 0, 0};
+    int j = 0;
+    for (; j <= size - 8; j += 8) {
+        v8f v;
+        memcpy(&v, x + j, sizeof v);
+        acc = v * v + acc;
+    }
+    float ss = hsum8(acc);
+    for (; j < size; j++)
+        ss += x[j] * x[j];
+    ss /= (float)size;
+    ss += 1e-5f;
+    const __m128 sv = _mm_set_ss(ss);
+    __m128 est = _mm_rsqrt_ss(sv);
+    const __m128 term = _mm_sub_ss(_mm_set_ss(3.0f), _mm_mul_ss(sv, _mm_mul_ss(est, est)));
+    est = _mm_mul_ss(_mm_mul_ss(_mm_set_ss(0.5f), est), term);
+    ss = _mm_cvtss_f32(est);
+    for (j = 0; j < size; j++)
+        o[j] = w[j] * (ss * x[j]);
+}
+
+/* FloatTransformer.cpp:240-382: W (d,n) @ x (n,) -> xout (d,), row-major W.
+ * Each row is a dot product with eight lane FMA accumulators, the reference's
+ * horizontal sum and the scalar tail (its 8-row blocking changes no row's
+ * sums); OpenMP over rows. */
+void oracle_matmul(float *xout, const float *x, const float *w, int n, int d)
+{
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < d; i++)
+        xout[i] = dot_ref(w + (size_t)i * n, x, n);
 }
 
 /* FloatTransformer.cpp:216-238: max seeded with x[0], exp(x - max), sum,

@@ -59,6 +59,10 @@ def lib():
         L.oracle_attention_step_mutant.argtypes = [_I] + step_args
         L.oracle_attention_step_mutant.restype = _I
         L.oracle_clear.argtypes = [_F, _F, ctypes.c_size_t]
+        L.oracle_rmsnorm.argtypes = [_F, _F, _F, _I]
+        L.oracle_rmsnorm.restype = None
+        L.oracle_matmul.argtypes = [_F, _F, _F, _I, _I]
+        L.oracle_matmul.restype = None
         L.oracle_set_threads.argtypes = [_I]
         L.oracle_max_threads.restype = _I
         _lib = L
@@ -81,6 +85,12 @@ def ref():
         L.leapref_run_layer.restype = _I
         L.leapref_clear_check.argtypes = [_I] * 5
         L.leapref_clear_check.restype = ctypes.c_long
+        L.leapref_rmsnorm.argtypes = [_F, _F, _F, _I]
+        L.leapref_rmsnorm.restype = _I
+        L.leapref_matmul.argtypes = [_F, _F, _F, _I, _I]
+        L.leapref_matmul.restype = _I
+        L.leapref_block.argtypes = [_I] * 7 + [_F] * 8
+        L.leapref_block.restype = _I
         _ref = L
     return _ref
 
@@ -91,6 +101,28 @@ def rope_table(seq_len: int, head_dim: int, theta: float = 500000.0):
     s = np.empty_like(c)
     lib().oracle_rope_table(seq_len, head_dim, theta, _fp(c), _fp(s))
     return c, s
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def rmsnorm(x, w):
+    """FloatTransformer.cpp:79-213 -> w * x / sqrt(mean(x^2) + 1e-5)."""
+    x, w = _c32(x).reshape(-1), _c32(w).reshape(-1)
+    o = np.empty_like(x)
+    lib().oracle_rmsnorm(_fp(o), _fp(x), _fp(w), x.size)
+    return o
+
+
+def matmul(w, x):
+    """FloatTransformer.cpp:240-382: W (d, n) @ x (n,) -> (d,)."""
+    w = _c32(w)
+    x = _c32(x).reshape(-1)
+    d, n = w.shape
+    o = np.empty(d, np.float32)
+    lib().oracle_matmul(_fp(o), _fp(x), _fp(w), n, d)
+    return o
 
 
 class Oracle:
@@ -132,6 +164,15 @@ class Oracle:
     def clear(self):
         lib().oracle_clear(_fp(self.key_cache), _fp(self.value_cache), self.key_cache.size)
 
+    def block(self, layer, pos, x, rms_att, wq, wk, wv, wo):
+        """run_layer up to the attention residual (FloatTransformer.cpp:394-683):
+        returns x + wo . attention(q, k, v) with q, k, v = W . rmsnorm(x)."""
+        x = _c32(x).reshape(-1)
+        xb = rmsnorm(x, rms_att)
+        q, k, v = matmul(wq, xb), matmul(wk, xb), matmul(wv, xb)
+        out, _ = self.step(layer, pos, q, k, v)
+        return x + matmul(wo, out)
+
 
 def ref_run_layer(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, wq, wk, wv,
                   key_cache, value_cache):
@@ -153,6 +194,36 @@ def ref_run_layer(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, wq
         raise RuntimeError("reference run_layer failed")
     outs["key_cache"], outs["value_cache"] = kc, vc
     return outs
+
+
+def ref_rmsnorm(x, w):
+    x, w = _c32(x).reshape(-1), _c32(w).reshape(-1)
+    o = np.empty_like(x)
+    ref().leapref_rmsnorm(_fp(o), _fp(x), _fp(w), x.size)
+    return o
+
+
+def ref_matmul(w, x):
+    w = _c32(w)
+    x = _c32(x).reshape(-1)
+    d, n = w.shape
+    o = np.empty(d, np.float32)
+    ref().leapref_matmul(_fp(o), _fp(x), _fp(w), n, d)
+    return o
+
+
+def ref_block(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, rms_att, wq, wk, wv, wo,
+              key_cache, value_cache):
+    """The reference's run_layer with the given attention weights and a zero
+    FFN: returns (x after the layer = x + wo . attention, key cache, value cache)."""
+    kc = np.array(key_cache, np.float32, copy=True)
+    vc = np.array(value_cache, np.float32, copy=True)
+    xo = np.array(x, np.float32, copy=True).reshape(-1)
+    rc = ref().leapref_block(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos,
+                             *(_fp(_c32(a)) for a in (rms_att, wq, wk, wv, wo)), _fp(kc), _fp(vc), _fp(xo))
+    if rc != 0:
+        raise RuntimeError("reference block failed")
+    return xo, kc, vc
 
 
 def ref_rope_table(dim, n_heads, seq_len):

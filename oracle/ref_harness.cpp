@@ -41,10 +41,12 @@ struct Weights {
 };
 
 // Lay out a weight blob in the order FloatTransformer::memory_map_weights
-// carves it (FloatTransformer.cpp:947-978) for one layer, with rms weights 1,
-// wq/wk/wv given, wo = identity and zero FFN/embedding/classifier.
+// carves it (FloatTransformer.cpp:947-978) for one layer, with wq/wk/wv given,
+// rms_att and wo given or (nullptr) ones and the identity, rms_ffn 1 and zero
+// FFN/embedding/classifier.
 std::unique_ptr<FloatTransformer> make_engine(const Config &c, const float *wq, const float *wk,
-                                              const float *wv, int layer, Weights &w)
+                                              const float *wv, int layer, Weights &w,
+                                              const float *rms_att = nullptr, const float *wo = nullptr)
 {
     const size_t dim = c.dim, L = c.n_layers, hd = c.dim / c.n_heads;
     const size_t kv_dim = (size_t)c.n_kv_heads * hd;
@@ -62,7 +64,11 @@ std::unique_ptr<FloatTransformer> make_engine(const Config &c, const float *wq, 
     std::memcpy(pwk + (size_t)layer * dim * kv_dim, wk, sizeof(float) * dim * kv_dim);
     std::memcpy(pwv + (size_t)layer * dim * kv_dim, wv, sizeof(float) * dim * kv_dim);
     float *wo_l = pwo + (size_t)layer * dim * dim;
-    for (size_t i = 0; i < dim; i++) wo_l[i * dim + i] = 1.0f;
+    if (wo)
+        std::memcpy(wo_l, wo, sizeof(float) * dim * dim);
+    else
+        for (size_t i = 0; i < dim; i++) wo_l[i * dim + i] = 1.0f;
+    if (rms_att) std::memcpy(p + (size_t)layer * dim, rms_att, sizeof(float) * dim);
     return std::make_unique<FloatTransformer>(c, -1, MAP_FAILED, 0, w.buf.data(), 1);
 }
 
@@ -137,6 +143,47 @@ int leapref_run_layer(int dim, int n_heads, int n_kv_heads, int n_layers, int se
         return 0;
     } catch (const std::exception &e) {
         std::cerr << "leapref_run_layer: " << e.what() << "\n";
+        return -1;
+    }
+}
+
+// The reference's rmsnorm (FloatTransformer.cpp:79-213) and matmul (:240-382).
+int leapref_rmsnorm(float *o, const float *x, const float *weight, int size)
+{
+    FloatTransformer::rmsnorm(o, x, weight, size);
+    return 0;
+}
+
+int leapref_matmul(float *xout, const float *x, const float *w, int n, int d)
+{
+    FloatTransformer::matmul(xout, x, w, n, d);
+    return 0;
+}
+
+// run_layer(layer, pos, x) with the given rms_att, wq, wk, wv and wo of the
+// layer and a zero FFN, so that x afterwards is x + wo . attention(...): the
+// attention sub-block with its residual (FloatTransformer.cpp:394-683; the
+// FFN adds w2 . (silu(w1 . xb) * (w3 . xb)) = 0).  key_cache/value_cache as
+// in leapref_run_layer; x is updated in place.
+int leapref_block(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len, int layer, int pos,
+                  const float *rms_att, const float *wq, const float *wk, const float *wv, const float *wo,
+                  float *key_cache, float *value_cache, float *x)
+{
+    try {
+        Config c = make_config(dim, n_heads, n_kv_heads, n_layers, seq_len);
+        const size_t hd = dim / n_heads, kv_dim = (size_t)n_kv_heads * hd;
+        const size_t cache_n = (size_t)n_layers * seq_len * kv_dim;
+        Weights w;
+        auto eng = make_engine(c, wq, wk, wv, layer, w, rms_att, wo);
+        if (eng->state.key_cache.size() != cache_n) throw std::runtime_error("cache size");
+        std::memcpy(eng->state.key_cache.data(), key_cache, sizeof(float) * cache_n);
+        std::memcpy(eng->state.value_cache.data(), value_cache, sizeof(float) * cache_n);
+        eng->run_layer(layer, pos, x);
+        std::memcpy(key_cache, eng->state.key_cache.data(), sizeof(float) * cache_n);
+        std::memcpy(value_cache, eng->state.value_cache.data(), sizeof(float) * cache_n);
+        return 0;
+    } catch (const std::exception &e) {
+        std::cerr << "leapref_block: " << e.what() << "\n";
         return -1;
     }
 }

@@ -57,3 +57,16 @@ def attention_f64(q_rot, k_rows, v_rows, n_heads, n_kv_heads, head_dim):
         p /= p.sum()
         out[h] = p @ V[:, g, :]
     return out.reshape(-1)
+
+
+def block_inputs(rng, dim, n_kv_dim):
+    """Seeded inputs of the attention sub-block: the residual stream x, the
+    rms_att weight (around 1) and the projections Wq [dim][dim],
+    Wk/Wv [kv_dim][dim], Wo [dim][dim] scaled by 1/sqrt(dim)."""
+    x = rng.standard_normal(dim).astype(np.float32)
+    rms = (1.0 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+    wq = normal(rng, (dim, dim), dim)
+    wk = normal(rng, (n_kv_dim, dim), dim)
+    wv = normal(rng, (n_kv_dim, dim), dim)
+    wo = normal(rng, (dim, dim), dim)
+    return x, rms, wq, wk, wv, wo

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import assert_close, attention_f64, normal, rel_err, rng_for, rope_f32
+from tests.helpers import assert_close, attention_f64, block_inputs, normal, rel_err, rng_for, rope_f32
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -87,8 +87,8 @@ def test_step_reference_golden(path):
     assert np.array_equal(q_rot, fx["q_rot"]), "rotated q differs from the reference"
     assert np.array_equal(k_slot, fx["k_slot"]), "rotated k in the cache differs"
     assert np.array_equal(v_slot, fx["v_slot"]), "v in the cache differs"
-    # observed 0 .. 3e-7: softmax reductions vectorised differently under -ffast-math
-    assert_close(out, fx["out"], rel=2e-6)
+    assert np.array_equal(out, fx["out"]), f"output differs: {rel_err(out, fx['out']):.2e}"
+
 
 
 @pytest.mark.parametrize("dim,nh,nkv,L,sl,layer,pos", [
@@ -115,7 +115,7 @@ def test_step_live_reference(dim, nh, nkv, L, sl, layer, pos):
     assert np.array_equal(q_rot, r["q_rot"])
     assert np.array_equal(orc.key_cache, r["key_cache"])
     assert np.array_equal(orc.value_cache, r["value_cache"])
-    assert_close(out, r["out"], rel=2e-6)
+    assert np.array_equal(out, r["out"]), f"output differs: {rel_err(out, r['out']):.2e}"
 
 
 def test_clear_matches_reference():
@@ -227,6 +227,126 @@ def test_relative_position_property():
         ref = score(d, 0)
         for m in (d + 5, d + 20, 60):
             assert abs(score(m, m - d) - ref) < 1e-5
+
+
+# ---- rmsnorm, matmul and the attention sub-block ---------------------------------
+
+def _block_fixture(path):
+    fx = _load(path)
+    dim, nh, nkv, L, sl, layer, pos = (int(v) for v in fx["dims"])
+    hd = dim // nh
+    x, rms, wq, wk, wv, wo = block_inputs(rng_for(*(int(k) for k in fx["key"])), dim, nkv * hd)
+    return fx, (dim, nh, nkv, L, sl, layer, pos), (x, rms, wq, wk, wv, wo)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "block_*.npz"))))
+def test_block_reference_golden(path):
+    fx, (dim, nh, nkv, L, sl, layer, pos), (x, rms, wq, wk, wv, wo) = _block_fixture(path)
+    xb = O.rmsnorm(x, rms)
+    assert np.array_equal(xb, fx["xb"]), "rmsnorm differs from the reference"
+    for w, key in ((wq, "q_pre"), (wk, "k_pre"), (wv, "v_pre")):
+        assert np.array_equal(O.matmul(w, xb), fx[key]), f"matmul ({key}) differs from the reference"
+    orc = O.Oracle(L, nh, nkv, dim // nh, sl)
+    orc.key_cache[layer, :pos] = fx["k_rows"]
+    orc.value_cache[layer, :pos] = fx["v_rows"]
+    got = orc.block(layer, pos, x, rms, wq, wk, wv, wo)
+    if (dim // nh) % 8 == 0:
+        assert np.array_equal(got, fx["x_out"]), f"block output differs: {rel_err(got, fx['x_out']):.2e}"
+        assert np.array_equal(orc.key_cache[layer, pos], fx["k_slot"])
+    else:
+        # head sizes off the 8-wide vectors leave scalar tails in the score,
+        # RoPE and weighted-V loops, whose -ffast-math vectorisation differs
+        # between the two builds in the last bit
+        assert_close(got, fx["x_out"], rel=1e-6)
+        assert_close(orc.key_cache[layer, pos], fx["k_slot"], rel=1e-6)
+    assert np.array_equal(orc.value_cache[layer, pos], fx["v_slot"])
+
+
+@pytest.mark.parametrize("n,d", [(8, 3), (7, 9), (100, 20), (2048, 64), (4096, 48)])
+def test_rmsnorm_matmul_live_reference(n, d):
+    if not O.ref_available():
+        pytest.skip("reference driver not built (reference sources absent)")
+    rng = rng_for(n, d, 5)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    assert np.array_equal(O.rmsnorm(x, w), O.ref_rmsnorm(x, w))
+    W = normal(rng, (d, n), n)
+    assert np.array_equal(O.matmul(W, x), O.ref_matmul(W, x))
+
+
+@pytest.mark.parametrize("dim,nh,nkv,L,sl,layer,pos", [(512, 4, 2, 2, 50, 1, 49), (256, 8, 8, 1, 9, 0, 5)])
+def test_block_live_reference(dim, nh, nkv, L, sl, layer, pos):
+    if not O.ref_available():
+        pytest.skip("reference driver not built (reference sources absent)")
+    hd = dim // nh
+    x, rms, wq, wk, wv, wo = block_inputs(rng_for(dim, pos, 3), dim, nkv * hd)
+    rng = rng_for(dim, pos, 4)
+    kc = normal(rng, (L, sl, nkv * hd), hd)
+    vc = normal(rng, (L, sl, nkv * hd), hd)
+    xr, kr, vr = O.ref_block(dim, nh, nkv, L, sl, layer, pos, x, rms, wq, wk, wv, wo, kc, vc)
+    orc = O.Oracle(L, nh, nkv, hd, sl)
+    orc.key_cache[:] = kc
+    orc.value_cache[:] = vc
+    assert np.array_equal(orc.block(layer, pos, x, rms, wq, wk, wv, wo), xr)
+    assert np.array_equal(orc.key_cache, kr) and np.array_equal(orc.value_cache, vr)
+
+
+def test_rmsnorm_closed_forms():
+    n = 64
+    for c in (1e-3, 0.5, 3.0, -7.0):
+        x = np.full(n, c, np.float32)
+        w = np.linspace(0.5, 2.0, n).astype(np.float32)
+        want = w.astype(np.float64) * c / np.sqrt(c * c + 1e-5)
+        assert rel_err(O.rmsnorm(x, w), want) < 1e-6
+    rng = rng_for(64, 1)
+    x = rng.standard_normal(n).astype(np.float32)
+    w = np.ones(n, np.float32)
+    # the float64 formula at two scales (the epsilon matters at the smaller
+    # one only), and mean(o^2) = m / (m + 1e-5) for unit weights
+    for a in (1.0, 1000.0):
+        xa = (a * x).astype(np.float32)
+        m = float(np.mean(xa.astype(np.float64) ** 2))
+        assert rel_err(O.rmsnorm(xa, w), xa.astype(np.float64) / np.sqrt(m + 1e-5)) < 1e-6
+        assert abs(float(np.mean(O.rmsnorm(xa, w).astype(np.float64) ** 2)) - m / (m + 1e-5)) < 1e-6
+
+
+def test_matmul_closed_forms():
+    rng = rng_for(77)
+    for n, d in ((16, 16), (100, 100), (37, 19)):
+        W = normal(rng, (d, n), n)
+        x = rng.standard_normal(n).astype(np.float32)
+        if n == d:
+            assert np.array_equal(O.matmul(np.eye(n, dtype=np.float32), x), x)
+        for j in (0, n // 2, n - 1):
+            e = np.zeros(n, np.float32)
+            e[j] = 1.0
+            assert np.array_equal(O.matmul(W, e), W[:, j])
+        assert rel_err(O.matmul(W, x), W.astype(np.float64) @ x) < 1e-6
+        y = rng.standard_normal(n).astype(np.float32)
+        assert rel_err(O.matmul(W, x + y), O.matmul(W, x).astype(np.float64) + O.matmul(W, y)) < 1e-5
+
+
+def test_projection_pins_catch_mistakes():
+    # a transposed weight, a dropped epsilon, a sum in place of the mean, a
+    # dropped residual: each fails at least one of the pins above
+    rng = rng_for(78)
+    n = 37
+    W = normal(rng, (n, n), n)
+    e = np.zeros(n, np.float32)
+    e[5] = 1.0
+    assert not np.array_equal(W.T @ e, O.matmul(W, e))
+    x = np.full(64, 1e-3, np.float32)
+    w = np.ones(64, np.float32)
+    good = O.rmsnorm(x, w)
+    assert rel_err(x / np.sqrt(np.mean(x ** 2)), good) > 1e-3          # no epsilon
+    assert rel_err(x / np.sqrt(np.sum(x ** 2) + 1e-5), good) > 1e-3    # sum, not mean
+    path = sorted(glob.glob(os.path.join(GOLDEN, "block_*.npz")))[0]
+    fx, (dim, nh, nkv, L, sl, layer, pos), (x, rms, wq, wk, wv, wo) = _block_fixture(path)
+    orc = O.Oracle(L, nh, nkv, dim // nh, sl)
+    orc.key_cache[layer, :pos] = fx["k_rows"]
+    orc.value_cache[layer, :pos] = fx["v_rows"]
+    no_residual = orc.block(layer, pos, x, rms, wq, wk, wv, wo) - x
+    assert rel_err(no_residual, fx["x_out"]) > 1e-2
 
 
 # ---- the pins catch plausible mistakes -------------------------------------------
