@@ -60,24 +60,35 @@ __device__ __forceinline__ float dot4f(float4 a, float4 b)
 
 typedef float gemv_f4 __attribute__((ext_vector_type(4)));
 
-// Dot products of rows [row0, row0 + RB) of w ([rows][n], row-major) with the
-// vector held as xv[c] = v4[tid + 256*c], c < NC (n = 1024 * NC).  Rows at or
-// past `rows` read the last row and are dropped by the caller.  Returns, in
-// thread i < RB, the dot product of row row0 + i.
+// Issue the loads of rows [row0, row0 + RB) of w ([rows][n], row-major) at
+// this thread's float4 columns tid + 256*c, c < NC (n = 1024 * NC).  Rows at
+// or past `rows` read the last row and are dropped by the caller.  Issued
+// before anything waits, so the weight stream starts with the kernel; the
+// weights are read once per step, so the loads are non-temporal (they do not
+// displace the KV rows and partials from L2; measured 0.7 us faster per
+// layer-step at Llama-3-8B).
 template <int RB, int NC>
-__device__ __forceinline__ float block_dots(const float *w, int rows, int row0, int n, const float4 (&xv)[NC],
-                                            float (*red)[kGemvWaves])
+__device__ __forceinline__ void issue_rows(const float *w, int rows, int row0, int n, gemv_f4 (&wv)[RB][NC])
 {
     const int tid = threadIdx.x;
-    const int lane = tid % 64, wave = tid / 64;
-    gemv_f4 wv[RB][NC];
 #pragma unroll
     for (int i = 0; i < RB; i++) {
         const int r = row0 + i;
         const gemv_f4 *wr = reinterpret_cast<const gemv_f4 *>(w + (size_t)(r < rows ? r : rows - 1) * n);
 #pragma unroll
-        for (int c = 0; c < NC; c++) wv[i][c] = wr[tid + kGemvThreads * c];
+        for (int c = 0; c < NC; c++) wv[i][c] = __builtin_nontemporal_load(wr + tid + kGemvThreads * c);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep every row load ahead of the vector work
+}
+
+// Dot products of the issued rows with the vector held as xv[c] = v4[tid +
+// 256*c].  Returns, in thread i < RB, the dot product of row row0 + i.
+template <int RB, int NC>
+__device__ __forceinline__ float finish_dots(const gemv_f4 (&wv)[RB][NC], const float4 (&xv)[NC],
+                                             float (*red)[kGemvWaves])
+{
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
 #pragma unroll
     for (int i = 0; i < RB; i++) {
         float s = 0.f;
@@ -99,7 +110,7 @@ __device__ __forceinline__ float block_dots(const float *w, int rows, int row0, 
 // q, k, v = W . rmsnorm(x).  rmsnorm: o = w * (x / sqrt(mean(x^2) + 1e-5))
 // (the reference's rsqrt estimate plus one Newton step rounds to within an
 // ulp or two of 1/sqrt).  Every workgroup normalises the (small) vector
-// itself, so no separate launch is needed.
+// itself while its weight rows are in flight, so no separate launch is needed.
 template <int RB, int NC>
 __global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
 {
@@ -109,27 +120,29 @@ __global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
     const int n = a.dim;
     const int rows = a.dim + 2 * a.kv_dim;
     const int row0 = blockIdx.x * RB;
+    gemv_f4 wv[RB][NC];
+    issue_rows<RB, NC>(a.w, rows, row0, n, wv);
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
     const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_w);
-    float4 xv[NC];
-    float ss = 0.f;
+    float4 xv[NC], gv[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
         xv[c] = x4[tid + kGemvThreads * c];
-        ss += dot4f(xv[c], xv[c]);
+        gv[c] = g4[tid + kGemvThreads * c];
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; c++) ss += dot4f(xv[c], xv[c]);
     ss = wave_sum(ss);
     if (tid % 64 == 0) ss_part[tid / 64] = ss;
     __syncthreads();
     ss = (ss_part[0] + ss_part[1]) + (ss_part[2] + ss_part[3]);
     const float scale = 1.0f / sqrtf(ss / (float)n + 1e-5f);
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-        const float4 g = g4[tid + kGemvThreads * c];
-        xv[c] = make_float4(g.x * (scale * xv[c].x), g.y * (scale * xv[c].y), g.z * (scale * xv[c].z),
-                            g.w * (scale * xv[c].w));
-    }
-    const float dot = block_dots<RB, NC>(a.w, rows, row0, n, xv, red);
+    for (int c = 0; c < NC; c++)
+        xv[c] = make_float4(gv[c].x * (scale * xv[c].x), gv[c].y * (scale * xv[c].y),
+                            gv[c].z * (scale * xv[c].z), gv[c].w * (scale * xv[c].w));
+    const float dot = finish_dots<RB, NC>(wv, xv, red);
     if (tid < RB) {
         const int r = row0 + tid;
         if (r < a.dim)
@@ -149,11 +162,13 @@ __global__ __launch_bounds__(kGemvThreads) void proj_residual_kernel(ProjArgs a)
     const int tid = threadIdx.x;
     const int n = NC * 4 * kGemvThreads;
     const int row0 = blockIdx.x * RB;
+    gemv_f4 wv[RB][NC];
+    issue_rows<RB, NC>(a.w, a.d, row0, n, wv);
     const float4 *v4 = reinterpret_cast<const float4 *>(a.xb);
     float4 xv[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) xv[c] = v4[tid + kGemvThreads * c];
-    const float dot = block_dots<RB, NC>(a.w, a.d, row0, n, xv, red);
+    const float dot = finish_dots<RB, NC>(wv, xv, red);
     if (tid < RB) {
         const int r = row0 + tid;
         if (r < a.d) a.x[r] += dot;

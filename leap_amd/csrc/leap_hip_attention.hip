@@ -179,12 +179,13 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     return 0;
 }
 
-// Projection kernels by dim = 1024 * NC; RB rows per workgroup keep 64 KiB of
-// weights in flight per workgroup.
+// Projection kernels by dim = 1024 * NC; RB rows per workgroup keep 128 KiB
+// of weights in flight per workgroup (64 KiB and 256 KiB measured slower at
+// Llama-3-8B).
 using QkvFn = void (*)(leap::QkvArgs);
 using ProjFn = void (*)(leap::ProjArgs);
 template <int NC>
-constexpr int proj_rows() { return 16 / NC; }
+constexpr int proj_rows() { return 32 / NC; }
 
 bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
 {
