@@ -46,6 +46,7 @@ constexpr int kCtrStride = 32;            // ints between arrival counters: one 
 constexpr int kCounters = (1 + kMaxSub) * kCtrStride;  // counter words per (sequence, KV head)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
+constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
 
 // Rows of one wave sub-tile: 16 (two MFMA row sets), i.e. 16 KiB of K and V
 // at head_dim 128, whatever the number of q heads per KV head.
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             const uint32_t roff = (uint32_t)(base + ks * 8 + krow) * row_bytes;
 #pragma unroll
             for (int f = 0; f < NF; f++)
-                kb[ks][f] = buf_load4(k_rsrc, roff + 16u * (uint32_t)(8 * f + ksl));
+                kb[ks][f] = buf_load4<kNt>(k_rsrc, roff + 16u * (uint32_t)(8 * f + ksl));
         }
     };
     auto load_v = [&](int sub) {
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const uint32_t roff = (uint32_t)(base + vs * RPV + vg) * row_bytes;
-            vb[vs] = buf_load4(v_rsrc, roff + 16u * (uint32_t)vj);
+            vb[vs] = buf_load4<kNt>(v_rsrc, roff + 16u * (uint32_t)vj);
         }
     };
     // q: rotate (fused multiply-adds are fine, q is not stored) and scale so
