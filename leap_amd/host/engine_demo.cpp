@@ -8,11 +8,16 @@
 // synthetic q/k/v in place of the projections (the GEMVs are outside the
 // path) and calls the shim for the attention block of every layer.
 //
-//   engine_demo n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir
+//   engine_demo n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block]
 //
 // writes, per (token, layer) in decode order, q|k|v|xb as raw fp32 to
 // out_dir/trace.bin so a checker can replay the same steps on a CPU
-// implementation.  Exit status: 0 success, 2 bad usage, 3 shim error.
+// implementation.  With `block`, the shim runs run_layer from its start to the
+// attention residual (:394-683) instead: the program generates each layer's
+// rms_att, wq, wk, wv, wo (written to out_dir/weights.bin in that order, per
+// layer), feeds the residual stream x from layer to layer and token to token,
+// and writes x before and after every (token, layer) to trace.bin.
+// Exit status: 0 success, 2 bad usage, 3 shim error.
 #include <cstdio>
 #include <cmath>
 #include <cstdint>
@@ -47,8 +52,10 @@ struct RunState {  // the attention-facing part of FloatRunState
 
 int main(int argc, char **argv)
 {
-    if (argc != 8) {
-        std::fprintf(stderr, "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir\n", argv[0]);
+    const bool block = argc == 9 && std::string(argv[8]) == "block";
+    if (argc != 8 && !block) {
+        std::fprintf(stderr, "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block]\n",
+                     argv[0]);
         return 2;
     }
     const int n_layers = std::atoi(argv[1]), n_heads = std::atoi(argv[2]), n_kv = std::atoi(argv[3]);
@@ -72,6 +79,37 @@ int main(int argc, char **argv)
         if (!f) {
             std::fprintf(stderr, "cannot write %s/trace.bin\n", out_dir.c_str());
             return 2;
+        }
+        if (block) {
+            std::FILE *wf = std::fopen((out_dir + "/weights.bin").c_str(), "wb");
+            if (!wf) {
+                std::fclose(f);
+                std::fprintf(stderr, "cannot write %s/weights.bin\n", out_dir.c_str());
+                return 2;
+            }
+            const float wscale = 1.0f / std::sqrt((float)dim);
+            std::vector<float> rms(dim), wq((size_t)dim * dim), wk((size_t)kv_dim * dim),
+                wv((size_t)kv_dim * dim), wo((size_t)dim * dim);
+            for (int l = 0; l < n_layers; l++) {  // the layer slices of FloatTransformerWeights
+                for (float &w : rms) w = 1.0f + rng.next(0.1f);
+                for (auto *m : {&wq, &wk, &wv, &wo})
+                    for (float &w : *m) w = rng.next(wscale);
+                attn.set_layer_weights(l, rms, wq, wk, wv, wo);
+                for (auto *m : {&rms, &wq, &wk, &wv, &wo}) std::fwrite(m->data(), 4, m->size(), wf);
+            }
+            std::fclose(wf);
+            std::vector<float> x(dim);
+            for (float &e : x) e = rng.next(1.0f);  // the token embedding row
+            for (int pos = 0; pos < n_tokens; pos++) {
+                for (int l = 0; l < n_layers; l++) {
+                    std::fwrite(x.data(), 4, x.size(), f);
+                    attn.block(l, pos, x);  // run_layer :394-683
+                    std::fwrite(x.data(), 4, x.size(), f);
+                }
+            }
+            std::fclose(f);
+            std::printf("engine_demo: %d tokens x %d layers done (sub-block)\n", n_tokens, n_layers);
+            return 0;
         }
         for (int pos = 0; pos < n_tokens; pos++) {      // generate(): one token per step
             for (int l = 0; l < n_layers; l++) {        // forward(): the layer loop

@@ -52,6 +52,29 @@ public:
         check(leap_hip_attention_step(h_, layer, pos, q.data(), k_new.data(), v_new.data(), out.data()), h_);
     }
 
+    // Weights of one held layer for block(): the layer's slices of
+    // FloatTransformerWeights (FloatTransformer.h:9-22), row-major.
+    void set_layer_weights(int layer, std::span<const float> rms_att, std::span<const float> wq,
+                           std::span<const float> wk, std::span<const float> wv, std::span<const float> wo)
+    {
+        const size_t dim = (size_t)q_dim_, kv = (size_t)kv_dim_;
+        if (rms_att.size() != dim || wq.size() != dim * dim || wk.size() != kv * dim || wv.size() != kv * dim ||
+            wo.size() != dim * dim)
+            throw std::invalid_argument("HipAttention::set_layer_weights: weight sizes do not match the model");
+        check(leap_hip_attention_set_layer_weights(h_, layer, rms_att.data(), wq.data(), wk.data(), wv.data(),
+                                                   wo.data()),
+              h_);
+    }
+
+    // run_layer(l, pos, x) from its start to the attention residual
+    // (FloatTransformer.cpp:394-683): x += Wo . attention(Wq/Wk/Wv . rmsnorm(x)).
+    void block(int layer, int pos, std::span<float> x)
+    {
+        if ((int)x.size() != q_dim_)
+            throw std::invalid_argument("HipAttention::block: x must hold dim floats");
+        check(leap_hip_attention_block(h_, layer, pos, x.data()), h_);
+    }
+
     // clear_kv_cache (FloatTransformer.cpp:74-77).
     void clear_kv_cache() { check(leap_hip_attention_clear(h_), h_); }
 

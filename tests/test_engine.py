@@ -47,3 +47,29 @@ def test_engine_demo_decode_matches_oracle(tmp_path, hip_device):
             q, k, v, xb = np.split(t, [nh * hd, nh * hd + nkv * hd, nh * hd + 2 * nkv * hd])
             want, _ = orc.step(layer, pos, q, k, v)
             assert_close(xb, want, what=f"token {pos} layer {layer}")
+
+
+@pytest.mark.gpu
+def test_engine_demo_block_matches_oracle(tmp_path, hip_device):
+    """The C++ wrapper's set_layer_weights/block path: 24 tokens x 2 layers of
+    run_layer up to the attention residual, x fed back from step to step."""
+    L, nh, nkv, hd, seq_len, n_tok = 2, 16, 4, 128, 32, 24
+    r = subprocess.run([_demo(), str(L), str(nh), str(nkv), str(hd), str(seq_len), str(n_tok),
+                        str(tmp_path), "block"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    dim, kv = nh * hd, nkv * hd
+    wall = np.fromfile(tmp_path / "weights.bin", dtype=np.float32)
+    sizes = [dim, dim * dim, kv * dim, kv * dim, dim * dim]
+    assert wall.size == L * sum(sizes)
+    weights = []
+    for part in np.split(wall, L):
+        rms, wq, wk, wv, wo = np.split(part, np.cumsum(sizes)[:-1])
+        weights.append((rms, wq.reshape(dim, dim), wk.reshape(kv, dim), wv.reshape(kv, dim),
+                        wo.reshape(dim, dim)))
+    trace = np.fromfile(tmp_path / "trace.bin", dtype=np.float32).reshape(n_tok, L, 2, dim)
+    orc = O.Oracle(L, nh, nkv, hd, seq_len)
+    for pos in range(n_tok):
+        for layer in range(L):
+            x_in, x_out = trace[pos, layer]
+            want = orc.block(layer, pos, x_in, *weights[layer])
+            assert_close(x_out - x_in, want - x_in, what=f"token {pos} layer {layer}")
