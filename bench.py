@@ -22,7 +22,10 @@ instead (rmsnorm, q/k/v projections, attention, wo projection and residual;
 three launches per layer-step), with synthetic N(0,1)/sqrt(dim) weights: one
 random set uploaded into every layer's own slot, so each layer streams its own
 copy from HBM.  Their bytes add the weights (Wq, Wk, Wv, Wo, rms) and the
-residual stream to B(T).
+residual stream to B(T).  The `*-q8-block-*` workloads run the quantized
+engine's sub-block: int8 weights with one float scale per group of 64 values
+(the reference exporter's default), the activations quantized per group on the
+device; their bytes count the int8 weights and their scales.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
 """
@@ -45,6 +48,10 @@ HBM_PEAK_GBS = 8000.0
 KERNEL = "decode_attention_kernel"
 BLOCK_METRIC = "attn sub-block (rmsnorm, qkv, attention, wo, residual) µs/layer-step + HBM GB/s, Llama-3-8B ctx 4096"
 BLOCK_KERNELS = "qkv_kernel + decode_attention_kernel + proj_residual_kernel"
+Q8_METRIC = ("attn sub-block, int8 weights (rmsnorm, quantize, W8A8 qkv, attention, quantize, W8A8 wo, residual) "
+             "µs/layer-step + HBM GB/s, Llama-3-8B ctx 4096")
+Q8_KERNELS = "q8_gemv_kernel (qkv) + decode_attention_kernel + q8_gemv_kernel (wo)"
+Q8_GROUP = 64
 SEED = 0x4C454150
 
 # name -> (layers, n_heads, n_kv_heads, head_dim, theta, batch, context, seed index)
@@ -56,11 +63,14 @@ WORKLOADS = {
     "llama3-70b-stage20-batch16": (20, 64, 8, 128, 500000.0, 16, 8192, 3),
     "llama3.1-8b-ctx131072": (32, 32, 8, 128, 500000.0, 1, 131072, 4),
     "llama3-8b-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 5),
+    "llama3-8b-q8-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 6),
 }
-BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096"}
+BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096", "llama3-8b-q8-block-ctx4096"}
+Q8_WORKLOADS = {"llama3-8b-q8-block-ctx4096"}
 DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3-8b-batch64-ragged": 10, "llama3-70b-stage20-batch16": 10,
-                 "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30}
+                 "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30,
+                 "llama3-8b-q8-block-ctx4096": 50}
 
 
 def algorithmic_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
@@ -77,6 +87,25 @@ def block_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
     written once."""
     dim, kv_dim = n_heads * hd, n_kv * hd
     return algorithmic_bytes(T, n_heads, n_kv, hd) + 4 * ((dim + 2 * kv_dim) * dim + dim * dim + dim) + 12 * dim
+
+
+def q8_block_bytes(T: int, n_heads: int, n_kv: int, hd: int, gs: int = Q8_GROUP) -> int:
+    """Bytes of one layer-step of the quantized engine's sub-block: the
+    attention's B(T), the int8 weights Wq, Wk, Wv, Wo with one 4-byte scale per
+    group of gs, rms_att, and the residual stream read twice and written once."""
+    dim, kv_dim = n_heads * hd, n_kv * hd
+    w = (dim + 2 * kv_dim) * dim + dim * dim
+    return algorithmic_bytes(T, n_heads, n_kv, hd) + w + 4 * (w // gs) + 4 * dim + 12 * dim
+
+
+def quantize_groups(w: np.ndarray, gs: int):
+    """Synthetic int8 weights in the quantized engine's format: int8 values
+    [d][n] and one float scale per group of gs values of a row (max|w| / 127,
+    values rounded to nearest)."""
+    g = w.reshape(-1, gs)
+    sc = (np.abs(g).max(axis=1) / 127.0).astype(np.float32)
+    q = np.rint(g / np.where(sc > 0, sc, 1.0)[:, None]).clip(-127, 127).astype(np.int8)
+    return q.reshape(w.shape), sc
 
 
 def traffic_from_profiles(workload: str):
@@ -97,7 +126,7 @@ def contexts(workload: str):
     return np.full(batch, ctx, np.int64)
 
 
-def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights):
+def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights, q8: bool = False):
     """The oracle's sub-block chain (rmsnorm, matmul, attention, matmul,
     residual), OpenMP over rows and heads, on the host, on layers
     [0, n_layers_sample) with the device cache bytes downloaded."""
@@ -121,10 +150,13 @@ def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float,
     while time.perf_counter() < t_end or len(times) < 3:
         t0 = time.perf_counter()
         for l in range(n_l):
-            orc.block(l, T - 1, x, *weights)
+            if q8:
+                orc.block_q8(l, T - 1, x, *weights, Q8_GROUP)
+            else:
+                orc.block(l, T - 1, x, *weights)
         times.append((time.perf_counter() - t0) / n_l)
     us = float(np.median(times)) * 1e6
-    gbs = block_bytes(T, nh, nkv, hd) / (us * 1e-6) / 1e9
+    gbs = (q8_block_bytes if q8 else block_bytes)(T, nh, nkv, hd) / (us * 1e-6) / 1e9
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "us_per_layer_step": round(us, 2),
@@ -247,8 +279,13 @@ def main():
             (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
             (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
         )
-        for l in range(L):
-            att.set_layer_weights(l, *weights)
+        if args.workload in Q8_WORKLOADS:
+            weights = (weights[0],) + tuple(quantize_groups(w, Q8_GROUP) for w in weights[1:])
+            for l in range(L):
+                att.set_layer_weights_q8(l, Q8_GROUP, *weights)
+        else:
+            for l in range(L):
+                att.set_layer_weights(l, *weights)
         x_res = torch.randn(dim, device=dev, generator=g)
         xp = x_res.data_ptr()
         pos = int(Ts[0]) - 1
@@ -291,7 +328,8 @@ def main():
 
     launches = steps * L
     us_layer = ms_total * 1e3 / launches
-    per_seq = block_bytes if is_block else algorithmic_bytes
+    is_q8 = args.workload in Q8_WORKLOADS
+    per_seq = q8_block_bytes if is_q8 else block_bytes if is_block else algorithmic_bytes
     bytes_layer = int(sum(per_seq(int(T), nh, nkv, hd) for T in Ts))
     gbs = bytes_layer / (us_layer * 1e-6) / 1e9
     if not np.isfinite((x_res if is_block else out).float().sum().item()):
@@ -299,7 +337,7 @@ def main():
         sys.exit(1)
 
     result = {
-        "metric": BLOCK_METRIC if is_block else METRIC,
+        "metric": Q8_METRIC if is_q8 else BLOCK_METRIC if is_block else METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -309,9 +347,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "int8+f32" if is_q8 else "f32",
         "data": (f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache generated on the device; "
-                 f"N(0,1)/sqrt(dim) weights, one set uploaded into every layer)") if is_block else
+                 f"N(0,1)/sqrt(dim) weights{f', int8 with one scale per {Q8_GROUP} values' if is_q8 else ''}, "
+                 f"one set uploaded into every layer)") if is_block else
                 f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache and q/k/v, generated on the device)",
         "config": {
             "workload": args.workload, "n_layers": L, "n_heads": nh, "n_kv_heads": nkv,
@@ -324,7 +363,7 @@ def main():
         "tokens_layers_per_s": round(batch * 1e6 / us_layer, 1),
         "host_wall_s": round(wall, 4),
         "roofline": {
-            "kernel": BLOCK_KERNELS if is_block else KERNEL,
+            "kernel": Q8_KERNELS if is_q8 else BLOCK_KERNELS if is_block else KERNEL,
             "bound": "hbm",
             "achieved": round(gbs, 2),
             "peak": HBM_PEAK_GBS,
@@ -340,7 +379,7 @@ def main():
         try:
             if is_block:
                 result["cpu_baseline"] = cpu_baseline_block(att, args.workload, Ts, args.cpu_layers,
-                                                            args.cpu_seconds, weights)
+                                                            args.cpu_seconds, weights, q8=is_q8)
             else:
                 result["cpu_baseline"] = cpu_baseline(att, args.workload, Ts, args.cpu_layers,
                                                       args.cpu_seconds)

@@ -139,12 +139,32 @@ int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const
  * :88-213), q, k, v = Wq, Wk, Wv . xb (:400-402, matmul :240-382), the
  * attention block of leap_hip_attention_step (k and v appended to
  * cache[layer][pos]), then x += Wo . out (:664-683).  x is the dim-float
- * residual stream, updated in place: a device pointer, enqueued on `stream`. */
+ * residual stream, updated in place: a device pointer, 16-byte aligned,
+ * enqueued on `stream`. */
 int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, float *x,
                                    void *stream);
 
 /* As leap_hip_attention_block_async with a host pointer, synchronous. */
 int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x);
+
+/* The quantized engine's weights of one held layer, for the same block calls:
+ * each projection is the reference's QuantizedTensor (QuantizedTransformer.h:
+ * 9-12; carved by init_quantized_tensors, QuantizedTransformer.cpp:88-100),
+ * int8 values [d][n] row-major plus one float scale per group of group_size
+ * consecutive values, [d*n/group_size]: wq/wo [dim][dim], wk/wv
+ * [kv_dim][dim]; rms_att [dim] fp32.  With these weights a block call runs
+ * QuantizedTransformer::run_layer from its start to the attention residual
+ * (QuantizedTransformer.cpp:654-936): xb = rmsnorm(x); quantize(xb) (:338-357);
+ * q, k, v = W8A8 matmul (:359-652); the fp32 attention step; quantize(out);
+ * x += Wo . out.  A handle holds either fp32 or int8 weights, fixed by its
+ * first set call, and one group size.  dim must be 2048, 4096 or 8192 and
+ * group_size a power of two with 4 <= group_size * 256 / dim <= 16 for dim
+ * 2048, 2 <= ... <= 16 for 4096, 1 <= ... <= 8 for 8192 (group sizes 32 to
+ * 128 or 256); others return -EINVAL. */
+int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, int group_size,
+                                            const float *rms_att, const int8_t *wq, const float *wq_s,
+                                            const int8_t *wk, const float *wk_s, const int8_t *wv,
+                                            const float *wv_s, const int8_t *wo, const float *wo_s);
 
 /* ---- Extras with no counterpart in the reference ---------------------- */
 
@@ -166,6 +186,22 @@ int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions);
  * their own device-side views of the cache. */
 int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,
                                      float **v);
+
+/* Device addresses of the sub-block's intermediate vectors as the last block
+ * call left them (valid until destroy; overwritten by the next call): the
+ * pre-RoPE q [dim], k and v [kv_dim] of the projections, the attention
+ * output att [dim] (the reference's s->xb before wo), and with int8 weights
+ * the quantized projection inputs xq/xs (rmsnorm output) and aq/as (the
+ * attention output): int8 [dim] and one scale per group (NULL with fp32
+ * weights).  For checking each stage of the block on its own. */
+typedef struct leap_hip_attention_block_views {
+    const float *q, *k, *v, *att;
+    const int8_t *xq;
+    const float *xs;
+    const int8_t *aq;
+    const float *as;
+} leap_hip_attention_block_views;
+int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention_block_views *out);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libleap_hip
 _F = ctypes.POINTER(ctypes.c_float)
 _I = ctypes.c_int
 _P = ctypes.c_void_p
+_B = ctypes.POINTER(ctypes.c_int8)
 
 EXPORTS = (
     "leap_hip_attention_create", "leap_hip_attention_destroy", "leap_hip_attention_last_error",
@@ -31,8 +32,15 @@ EXPORTS = (
     "leap_hip_attention_kv_fill_normal", "leap_hip_attention_rope_download",
     "leap_hip_attention_set_split", "leap_hip_attention_kv_device_ptr",
     "leap_hip_attention_set_layer_weights", "leap_hip_attention_block",
-    "leap_hip_attention_block_async",
+    "leap_hip_attention_block_async", "leap_hip_attention_set_layer_weights_q8",
+    "leap_hip_attention_block_views_get",
 )
+
+
+class BlockViews(ctypes.Structure):
+    """leap_hip_attention_block_views: device addresses of the sub-block's
+    intermediates after the last block call."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "att", "xq", "xs", "aq", "as_")]
 
 
 class LeapError(RuntimeError):
@@ -82,6 +90,8 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_set_layer_weights.argtypes = [H, _I, _F, _F, _F, _F, _F]
     L.leap_hip_attention_block.argtypes = [H, _I, _I, _F]
     L.leap_hip_attention_block_async.argtypes = [H, _I, _I, _P, _P]
+    L.leap_hip_attention_set_layer_weights_q8.argtypes = [H, _I, _I, _F] + [_B, _F] * 4
+    L.leap_hip_attention_block_views_get.argtypes = [H, ctypes.POINTER(BlockViews)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -179,6 +189,27 @@ class HipAttention:
         d, kv = self.q_dim, self.kv_dim
         arrs = (_f32(rms_att, d), _f32(wq, d * d), _f32(wk, kv * d), _f32(wv, kv * d), _f32(wo, d * d))
         self._check(self.lib.leap_hip_attention_set_layer_weights(self.h, layer, *(_fp(a) for a in arrs)))
+
+    def set_layer_weights_q8(self, layer, group_size, rms_att, wq, wk, wv, wo):
+        """Upload one layer's int8 weights: each of wq, wk, wv, wo is (int8
+        values [d][n], float scales [d*n/group_size]) as the quantized engine
+        holds them."""
+        d, kv = self.q_dim, self.kv_dim
+        arrs = [_f32(rms_att, d)]  # held here until the upload returns
+        for (q, sc), rows in ((wq, d), (wk, kv), (wv, kv), (wo, d)):
+            q = np.ascontiguousarray(q, np.int8).reshape(-1)
+            if q.size != rows * d:
+                raise ValueError(f"expected {rows * d} int8 values, got {q.size}")
+            arrs += [q, _f32(sc, rows * d // group_size)]
+        args = [a.ctypes.data_as(_B) if a.dtype == np.int8 else _fp(a) for a in arrs]
+        self._check(self.lib.leap_hip_attention_set_layer_weights_q8(self.h, layer, group_size, *args))
+
+    def block_views(self) -> dict:
+        """Device addresses of the last block call's intermediates
+        (q, k, v, att; xq, xs, aq, as_ with int8 weights, else None)."""
+        bv = BlockViews()
+        self._check(self.lib.leap_hip_attention_block_views_get(self.h, ctypes.byref(bv)))
+        return {n: getattr(bv, n) for n, _ in BlockViews._fields_}
 
     def block(self, layer, pos, x):
         """x + Wo . attention(Wq/Wk/Wv . rmsnorm(x)); returns the new residual stream."""

@@ -14,12 +14,15 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <new>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "decode_attention.hpp"
 #include "gemv.hpp"
+#include "gemv_q8.hpp"
 
 extern "C" void leap_rope_table_host(int seq_len, int head_size, float theta, float *cos_tab,
                                      float *sin_tab);
@@ -44,6 +47,16 @@ struct leap_hip_attention {
     float *w_rms = nullptr;   // [n_local][dim]
     std::vector<char> w_set;  // per held layer: weights uploaded
     float *blk = nullptr;     // q [dim] | k [kv_dim] | v [kv_dim] | xb [dim] | x staging [dim]
+    // int8 weights of the quantized engine (one format per handle: the first
+    // set_layer_weights* call fixes it) with one float scale per group of gs
+    int w_fmt = 0;            // 0 none yet, 1 fp32, 2 int8
+    int gs = 0;
+    int8_t *w8_qkv = nullptr; // [n_local][dim + 2*kv_dim][dim]
+    float *s8_qkv = nullptr;  // [n_local][dim + 2*kv_dim][dim / gs]
+    int8_t *w8_o = nullptr;   // [n_local][dim][dim]
+    float *s8_o = nullptr;    // [n_local][dim][dim / gs]
+    int8_t *q8_act = nullptr; // xq [dim] | aq [dim]: the quantized projection inputs of the last block
+    float *q8_act_s = nullptr;// xs [dim / gs] | as [dim / gs]: their group scales
     hipStream_t stream = nullptr;
     int split = 0;
     int n_cu = 256;  // compute units of the device
@@ -179,6 +192,27 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     return 0;
 }
 
+// Allocate every (pointer, bytes) pair or none of them: on a failure the
+// ones already made are freed and the pointers stay null, so a later call
+// starts over instead of finding half a set.
+int alloc_all(leap_hip_attention *h, std::initializer_list<std::pair<void **, size_t>> bufs)
+{
+    std::vector<void *> made;
+    for (const auto &b : bufs) {
+        void *p = nullptr;
+        const hipError_t e = hipMalloc(&p, b.second);
+        if (e != hipSuccess) {
+            for (void *q : made) (void)hipFree(q);
+            return set_err(h, e == hipErrorOutOfMemory ? -ENOMEM : -EIO, "hipMalloc(%zu bytes): %s", b.second,
+                           hipGetErrorString(e));
+        }
+        made.push_back(p);
+    }
+    size_t i = 0;
+    for (const auto &b : bufs) *b.first = made[i++];
+    return 0;
+}
+
 // Projection kernels by dim = 1024 * NC; RB rows per workgroup keep 128 KiB
 // of weights in flight per workgroup (64 KiB and 256 KiB measured slower at
 // Llama-3-8B).
@@ -201,16 +235,79 @@ bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
     return false;
 }
 
+// Quantized projections by n = 256 * E values per row (E per thread) and
+// group size gs = L * E; RB rows per workgroup.
+using Q8Fn = void (*)(leap::Q8Args);
+
+template <int E, int L>
+constexpr int q8_rows() { return E >= 32 ? 8 : 16; }
+
+bool pick_q8(int dim, int gs, Q8Fn *qkv, Q8Fn *proj, int *rb)
+{
+#define LEAP_Q8(E, L)                                                                  \
+    if (dim == 256 * E && gs == L * E) {                                               \
+        *qkv = leap::q8_gemv_kernel<E, L, q8_rows<E, L>(), true, false>;               \
+        *proj = leap::q8_gemv_kernel<E, L, q8_rows<E, L>(), false, true>;              \
+        *rb = q8_rows<E, L>();                                                         \
+        return true;                                                                   \
+    }
+    LEAP_Q8(8, 4) LEAP_Q8(8, 8) LEAP_Q8(8, 16)
+    LEAP_Q8(16, 2) LEAP_Q8(16, 4) LEAP_Q8(16, 8) LEAP_Q8(16, 16)
+    LEAP_Q8(32, 1) LEAP_Q8(32, 2) LEAP_Q8(32, 4) LEAP_Q8(32, 8)
+#undef LEAP_Q8
+    return false;
+}
+
+int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, hipStream_t stream)
+{
+    Q8Fn qkv, proj;
+    int rb;
+    const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs;
+    if (!pick_q8(dim, gs, &qkv, &proj, &rb))
+        return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
+    float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
+    const size_t rows_qkv = (size_t)(dim + 2 * kv);
+    leap::Q8Args qa{};
+    qa.x = x;
+    qa.rms_w = h->w_rms + (size_t)li * dim;
+    qa.w = h->w8_qkv + (size_t)li * rows_qkv * dim;
+    qa.ws = h->s8_qkv + (size_t)li * rows_qkv * (dim / gs);
+    qa.out0 = q;
+    qa.out1 = k;
+    qa.out2 = v;
+    qa.rows = (int)rows_qkv;
+    qa.n0 = dim;
+    qa.n1 = kv;
+    qa.xq_out = h->q8_act;
+    qa.xs_out = h->q8_act_s;
+    hipLaunchKernelGGL(qkv, dim3((unsigned)((rows_qkv + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, qa);
+    HIP_TRY(h, hipGetLastError());
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
+    leap::Q8Args pa{};
+    pa.x = xb;
+    pa.w = h->w8_o + (size_t)li * dim * dim;
+    pa.ws = h->s8_o + (size_t)li * dim * (dim / gs);
+    pa.out0 = x;
+    pa.rows = dim;
+    pa.n0 = dim;
+    pa.xq_out = h->q8_act + dim;
+    pa.xs_out = h->q8_act_s + dim / gs;
+    hipLaunchKernelGGL(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, pa);
+    HIP_TRY(h, hipGetLastError());
+    return 0;
+}
+
 int launch_block(leap_hip_attention *h, int layer, int pos, float *x, hipStream_t stream)
 {
+    const int li = layer - h->cfg.layer_begin;
+    if (h->w_fmt == 0 || !h->w_set[li]) return set_err(h, -EINVAL, "no weights set for layer %d", layer);
+    if (h->w_fmt == 2) return launch_block_q8(h, li, layer, pos, x, stream);
     QkvFn qkv;
     ProjFn proj;
     int rb;
     const int dim = h->q_dim, kv = h->kv_dim;
     if (!pick_proj(dim, &qkv, &proj, &rb))
         return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
-    const int li = layer - h->cfg.layer_begin;
-    if (!h->w_qkv || !h->w_set[li]) return set_err(h, -EINVAL, "no weights set for layer %d", layer);
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
     leap::QkvArgs qa{};
     qa.x = x;
@@ -340,7 +437,7 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->pos_dev,
                     h->q_dev,   h->k_dev,   h->v_dev, h->out_dev, h->blk,  h->w_qkv,    h->w_o,
-                    h->w_rms};
+                    h->w_rms,   h->w8_qkv,  h->s8_qkv, h->w8_o, h->s8_o, h->q8_act, h->q8_act_s};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
@@ -459,12 +556,15 @@ int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const
     const int dim = h->q_dim, kv = h->kv_dim;
     if (!pick_proj(dim, &qkv, &proj, &rb))
         return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
+    if (h->w_fmt == 2) return set_err(h, -EINVAL, "this handle holds int8 weights");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     const size_t n_qkv = (size_t)(dim + 2 * kv) * dim, n_o = (size_t)dim * dim;
     if (!h->w_qkv) {
-        HIP_TRY(h, hipMalloc(&h->w_qkv, (size_t)h->n_local * n_qkv * sizeof(float)));
-        HIP_TRY(h, hipMalloc(&h->w_o, (size_t)h->n_local * n_o * sizeof(float)));
-        HIP_TRY(h, hipMalloc(&h->w_rms, (size_t)h->n_local * dim * sizeof(float)));
+        if (int rc = alloc_all(h, {{(void **)&h->w_qkv, (size_t)h->n_local * n_qkv * sizeof(float)},
+                                   {(void **)&h->w_o, (size_t)h->n_local * n_o * sizeof(float)},
+                                   {(void **)&h->w_rms, (size_t)h->n_local * dim * sizeof(float)}}))
+            return rc;
+        h->w_fmt = 1;
     }
     const int li = layer - h->cfg.layer_begin;
     float *dq = h->w_qkv + (size_t)li * n_qkv;
@@ -482,6 +582,77 @@ int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const
     return 0;
 }
 
+int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, int group_size,
+                                            const float *rms_att, const int8_t *wq, const float *wq_s,
+                                            const int8_t *wk, const float *wk_s, const int8_t *wv,
+                                            const float *wv_s, const int8_t *wo, const float *wo_s)
+{
+    if (!h) return -EINVAL;
+    if (int rc = check_layer(h, layer)) return rc;
+    if (!rms_att || !wq || !wq_s || !wk || !wk_s || !wv || !wv_s || !wo || !wo_s)
+        return set_err(h, -EINVAL, "NULL weight");
+    Q8Fn qkv, proj;
+    int rb;
+    const int dim = h->q_dim, kv = h->kv_dim, gs = group_size;
+    if (!pick_q8(dim, gs, &qkv, &proj, &rb))
+        return set_err(h, -EINVAL,
+                       "dim %d with group size %d: the int8 projections need dim in {2048, 4096, 8192} and "
+                       "a group of 4 to 16 threads' values (2048: 32-128, 4096: 32-256, 8192: 32-256)",
+                       dim, gs);
+    if (h->w_fmt == 1) return set_err(h, -EINVAL, "this handle holds fp32 weights");
+    if (h->w_fmt == 2 && gs != h->gs)
+        return set_err(h, -EINVAL, "group size %d differs from the handle's %d", gs, h->gs);
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    const size_t rows_qkv = (size_t)(dim + 2 * kv), ng = (size_t)(dim / gs);
+    if (!h->w8_qkv) {
+        if (int rc = alloc_all(h, {{(void **)&h->w8_qkv, (size_t)h->n_local * rows_qkv * dim},
+                                   {(void **)&h->s8_qkv, (size_t)h->n_local * rows_qkv * ng * sizeof(float)},
+                                   {(void **)&h->w8_o, (size_t)h->n_local * dim * dim},
+                                   {(void **)&h->s8_o, (size_t)h->n_local * dim * ng * sizeof(float)},
+                                   {(void **)&h->w_rms, (size_t)h->n_local * dim * sizeof(float)},
+                                   {(void **)&h->q8_act, (size_t)2 * dim},
+                                   {(void **)&h->q8_act_s, 2 * ng * sizeof(float)}}))
+            return rc;
+        h->gs = gs;
+        h->w_fmt = 2;
+    }
+    const int li = layer - h->cfg.layer_begin;
+    int8_t *dq = h->w8_qkv + (size_t)li * rows_qkv * dim;
+    float *ds = h->s8_qkv + (size_t)li * rows_qkv * ng;
+    hipStream_t s = h->stream;
+    const size_t nq = (size_t)dim * dim, nk = (size_t)kv * dim;
+    HIP_TRY(h, hipMemcpyAsync(dq, wq, nq, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(dq + nq, wk, nk, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(dq + nq + nk, wv, nk, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(ds, wq_s, nq / gs * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(ds + nq / gs, wk_s, nk / gs * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(ds + (nq + nk) / gs, wv_s, nk / gs * sizeof(float), hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->w8_o + (size_t)li * nq, wo, nq, hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->s8_o + (size_t)li * nq / gs, wo_s, nq / gs * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipMemcpyAsync(h->w_rms + (size_t)li * dim, rms_att, (size_t)dim * sizeof(float),
+                              hipMemcpyHostToDevice, s));
+    HIP_TRY(h, hipStreamSynchronize(s));
+    h->w_set[li] = 1;
+    return 0;
+}
+
+int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention_block_views *out)
+{
+    if (!h) return -EINVAL;
+    if (!out) return set_err(h, -EINVAL, "NULL output");
+    const int dim = h->q_dim, kv = h->kv_dim;
+    out->q = h->blk;
+    out->k = h->blk + dim;
+    out->v = h->blk + dim + kv;
+    out->att = h->blk + dim + 2 * kv;
+    out->xq = h->q8_act;
+    out->xs = h->q8_act_s;
+    out->aq = h->q8_act ? h->q8_act + dim : nullptr;
+    out->as = h->q8_act_s ? h->q8_act_s + dim / h->gs : nullptr;
+    return 0;
+}
+
 int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, float *x, void *stream)
 {
     if (!h) return -EINVAL;
@@ -489,6 +660,7 @@ int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, fl
     if (pos < 0 || pos >= h->cfg.seq_len)
         return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
     if (!x) return set_err(h, -EINVAL, "NULL buffer");
+    if (reinterpret_cast<uintptr_t>(x) % 16) return set_err(h, -EINVAL, "x must be 16-byte aligned");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     return launch_block(h, layer, pos, x, (hipStream_t)stream);
 }

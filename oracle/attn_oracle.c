@@ -34,6 +34,15 @@
  *                         normalises to w / sqrt(1 + 1e-5/c^2) * sign, an
  *                         identity matrix returns x, a one-hot x returns a
  *                         column of W, linearity in x.
+ *   oracle_quantize,      bitwise against the reference's own quantize and
+ *   oracle_matmul_q8      W8A8 matmul (oracle/_ref q8 harness, committed
+ *                         golden fixtures); closed forms: the group maximum
+ *                         maps to +-127, exact halves round away from zero,
+ *                         an all-zero group has scale 0, dequantised values
+ *                         lie within scale/2 of x; the matmul equals the
+ *                         float64 sum of exact integer group dots times the
+ *                         scales to within float rounding, one-hot x returns
+ *                         a dequantised column.
  *   oracle_attention_step against the reference's run_layer (oracle/_ref
  *                         harness, committed golden fixtures), float64
  *                         brute force on tiny shapes, and closed forms
@@ -159,6 +168,54 @@ void oracle_matmul(float *xout, const float *x, const float *w, int n, int d)
 #pragma omp parallel for schedule(static)
     for (int i = 0; i < d; i++)
         xout[i] = dot_ref(w + (size_t)i * n, x, n);
+}
+
+/* QuantizedTransformer.cpp:338-357.  Per group of gs values (the last group
+ * may be shorter): scale = max|x| / 127, id = 1 / scale (0 for an all-zero
+ * group), q = round-half-away-from-zero(x * id).  The reference's release
+ * flags (-ffast-math: reciprocal-math) turn the division by the constant 127
+ * into a product with its float reciprocal; the restatement writes that
+ * product out so that the scales agree bit for bit. */
+void oracle_quantize(const float *x, int n, int gs, int8_t *q, float *s)
+{
+    for (int i = 0; i < n; i += gs) {
+        const int cur = gs < n - i ? gs : n - i;
+        float max_val = 0.0f;
+        for (int j = 0; j < cur; j++) {
+            const float a = fabsf(x[i + j]);
+            if (a > max_val) max_val = a;
+        }
+        const float scale = max_val * (1.0f / 127.0f);
+        const float id = scale != 0.0f ? 1.0f / scale : 0.0f;
+        s[i / gs] = scale;
+        for (int j = 0; j < cur; j++) q[i + j] = (int8_t)roundf(x[i + j] * id);
+    }
+}
+
+/* QuantizedTransformer.cpp:359-652.  xout[i] = sum over the whole groups g of
+ * row i, in order, of idot_g * (ws_g * sx_g): the int8 dot product of a
+ * group is exact in int32 (the reference's madd/add tree or dot-product
+ * instructions give the same integer), and the float accumulation is one
+ * fused multiply-add per group, val = fma((float)idot, ws * sx, val).  That is
+ * how the reference's release build evaluates `val += (float)ival * ws * sx`
+ * (-ffast-math reassociates the product and contracts the sum; measured
+ * bitwise against the compiled reference).  The weight scale of (row i,
+ * column j) is ws[(i*n + j) / gs], elements past the last whole group of a
+ * row are not used (the reference's loop bound j <= n - gs). */
+void oracle_matmul_q8(float *xout, const int8_t *xq, const float *xs, const int8_t *wq, const float *ws, int n,
+                      int d, int gs)
+{
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < d; i++) {
+        const size_t in = (size_t)i * n;
+        float val = 0.0f;
+        for (int j = 0; j <= n - gs; j += gs) {
+            int32_t ival = 0;
+            for (int k = 0; k < gs; k++) ival += (int32_t)xq[j + k] * (int32_t)wq[in + j + k];
+            val = fmaf((float)ival, ws[(in + j) / gs] * xs[j / gs], val);
+        }
+        xout[i] = val;
+    }
 }
 
 /* FloatTransformer.cpp:216-238: max seeded with x[0], exp(x - max), sum,

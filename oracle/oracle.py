@@ -3,7 +3,8 @@
 ctypes bindings for the CPU restatement (``liboracle_attn.so``, built from
 ``attn_oracle.c``) and for the driver around the reference's own code
 (``_ref/libleap_ref.so``, built from ``ref_harness.cpp`` plus the reference's
-``src/inference/FloatTransformer.cpp``).  Only the tests, the smoke check and
+``src/inference/FloatTransformer.cpp``; ``_ref/libleap_ref_q8.so``, built from
+``ref_harness_q8.cpp`` plus ``src/inference/QuantizedTransformer.cpp``).  Only the tests, the smoke check and
 the CPU-baseline leg of the benchmark import this module; the product package
 ``leap_amd`` never does.
 """
@@ -18,10 +19,12 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle_attn.so")
 REF_SO = os.path.join(HERE, "_ref", "libleap_ref.so")
+REF_Q8_SO = os.path.join(HERE, "_ref", "libleap_ref_q8.so")
 REF_SRC = "/root/reference/src/inference"
 
 _F = ctypes.POINTER(ctypes.c_float)
 _I = ctypes.c_int
+_B = ctypes.POINTER(ctypes.c_int8)
 
 
 def build(ref: bool | None = None) -> None:
@@ -41,8 +44,14 @@ def _fp(a: np.ndarray):
     return a.ctypes.data_as(_F)
 
 
+def _bp(a: np.ndarray):
+    assert a.dtype == np.int8 and a.flags.c_contiguous
+    return a.ctypes.data_as(_B)
+
+
 _lib = None
 _ref = None
+_ref_q8 = None
 
 
 def lib():
@@ -63,6 +72,10 @@ def lib():
         L.oracle_rmsnorm.restype = None
         L.oracle_matmul.argtypes = [_F, _F, _F, _I, _I]
         L.oracle_matmul.restype = None
+        L.oracle_quantize.argtypes = [_F, _I, _I, _B, _F]
+        L.oracle_quantize.restype = None
+        L.oracle_matmul_q8.argtypes = [_F, _B, _F, _B, _F, _I, _I, _I]
+        L.oracle_matmul_q8.restype = None
         L.oracle_set_threads.argtypes = [_I]
         L.oracle_max_threads.restype = _I
         _lib = L
@@ -95,6 +108,26 @@ def ref():
     return _ref
 
 
+def ref_q8_available() -> bool:
+    return os.path.isfile(REF_Q8_SO)
+
+
+def ref_q8():
+    global _ref_q8
+    if _ref_q8 is None:
+        if not ref_q8_available():
+            raise RuntimeError(f"reference driver missing: {REF_Q8_SO}")
+        L = ctypes.CDLL(REF_Q8_SO)
+        L.leapref_q8_quantize.argtypes = [_F, _I, _I, _B, _F]
+        L.leapref_q8_quantize.restype = _I
+        L.leapref_q8_matmul.argtypes = [_F, _B, _F, _B, _F, _I, _I, _I]
+        L.leapref_q8_matmul.restype = _I
+        L.leapref_q8_block.argtypes = [_I] * 8 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _F]
+        L.leapref_q8_block.restype = _I
+        _ref_q8 = L
+    return _ref_q8
+
+
 def rope_table(seq_len: int, head_dim: int, theta: float = 500000.0):
     """FloatTransformer.cpp:56-72 -> (cos, sin), each [seq_len, head_dim/2] fp32."""
     c = np.empty((seq_len, head_dim // 2), np.float32)
@@ -122,6 +155,36 @@ def matmul(w, x):
     d, n = w.shape
     o = np.empty(d, np.float32)
     lib().oracle_matmul(_fp(o), _fp(x), _fp(w), n, d)
+    return o
+
+
+def quantize(x, gs: int):
+    """QuantizedTransformer.cpp:338-357 -> (int8 values [n], scales [ceil(n/gs)])."""
+    x = _c32(x).reshape(-1)
+    q = np.empty(x.size, np.int8)
+    sc = np.empty(-(-x.size // gs), np.float32)
+    lib().oracle_quantize(_fp(x), x.size, gs, _bp(q), _fp(sc))
+    return q, sc
+
+
+def quantize_weight(w, gs: int):
+    """A weight matrix [d, n] (n a multiple of gs) in the quantized engine's
+    format: int8 values [d, n] and one scale per group of a row, [d * n / gs]
+    (the QuantizedTensor layout, QuantizedTransformer.h:9-12)."""
+    w = _c32(w)
+    assert w.ndim == 2 and w.shape[1] % gs == 0
+    q, sc = quantize(w.reshape(-1), gs)
+    return q.reshape(w.shape), sc
+
+
+def matmul_q8(wq, ws, xq, xs, gs: int):
+    """QuantizedTransformer.cpp:359-652: int8 W [d, n] with group scales ws,
+    int8 x [n] with group scales xs -> float [d]."""
+    wq = np.ascontiguousarray(wq, np.int8)
+    d, n = wq.shape
+    o = np.empty(d, np.float32)
+    lib().oracle_matmul_q8(_fp(o), _bp(np.ascontiguousarray(xq, np.int8)), _fp(_c32(xs)), _bp(wq),
+                           _fp(_c32(ws)), n, d, gs)
     return o
 
 
@@ -173,6 +236,23 @@ class Oracle:
         out, _ = self.step(layer, pos, q, k, v)
         return x + matmul(wo, out)
 
+    def block_q8(self, layer, pos, x, rms_att, wq, wk, wv, wo, gs, stages: bool = False):
+        """The quantized engine's run_layer up to the attention residual
+        (QuantizedTransformer.cpp:654-...): xb = rmsnorm(x), quantized per
+        group; q, k, v = W8A8 matmuls; the fp32 attention step; its output
+        quantized; x + wo . that.  Each weight is (int8 [d, n], scales).
+        Returns x_out, or with stages=True a dict of every intermediate."""
+        x = _c32(x).reshape(-1)
+        xb = rmsnorm(x, rms_att)
+        xq, xs = quantize(xb, gs)
+        q, k, v = (matmul_q8(w[0], w[1], xq, xs, gs) for w in (wq, wk, wv))
+        att, _ = self.step(layer, pos, q, k, v)
+        aq, as_ = quantize(att, gs)
+        x_out = x + matmul_q8(wo[0], wo[1], aq, as_, gs)
+        if not stages:
+            return x_out
+        return dict(xb=xb, xq=xq, xs=xs, q=q, k=k, v=v, att=att, aq=aq, as_=as_, x_out=x_out)
+
 
 def ref_run_layer(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, wq, wk, wv,
                   key_cache, value_cache):
@@ -223,6 +303,43 @@ def ref_block(dim, n_heads, n_kv_heads, n_layers, seq_len, layer, pos, x, rms_at
                              *(_fp(_c32(a)) for a in (rms_att, wq, wk, wv, wo)), _fp(kc), _fp(vc), _fp(xo))
     if rc != 0:
         raise RuntimeError("reference block failed")
+    return xo, kc, vc
+
+
+def ref_q8_quantize(x, gs: int):
+    x = _c32(x).reshape(-1)
+    q = np.empty(x.size, np.int8)
+    sc = np.empty(-(-x.size // gs), np.float32)
+    if ref_q8().leapref_q8_quantize(_fp(x), x.size, gs, _bp(q), _fp(sc)) != 0:
+        raise RuntimeError("reference quantize failed")
+    return q, sc
+
+
+def ref_q8_matmul(wq, ws, xq, xs, gs: int):
+    wq = np.ascontiguousarray(wq, np.int8)
+    d, n = wq.shape
+    o = np.empty(d, np.float32)
+    if ref_q8().leapref_q8_matmul(_fp(o), _bp(np.ascontiguousarray(xq, np.int8)), _fp(_c32(xs)), _bp(wq),
+                                  _fp(_c32(ws)), n, d, gs) != 0:
+        raise RuntimeError("reference q8 matmul failed")
+    return o
+
+
+def ref_q8_block(dim, n_heads, n_kv_heads, n_layers, seq_len, gs, layer, pos, x, rms_att, wq, wk, wv, wo,
+                 key_cache, value_cache):
+    """The quantized reference's run_layer with the given attention weights
+    (each (int8 [d, n], scales)) and a zero FFN: returns (x after the layer,
+    key cache, value cache)."""
+    kc = np.array(key_cache, np.float32, copy=True)
+    vc = np.array(value_cache, np.float32, copy=True)
+    xo = np.array(x, np.float32, copy=True).reshape(-1)
+    ws = []
+    for w in (wq, wk, wv, wo):
+        ws += [_bp(np.ascontiguousarray(w[0], np.int8)), _fp(_c32(w[1]))]
+    rc = ref_q8().leapref_q8_block(dim, n_heads, n_kv_heads, n_layers, seq_len, gs, layer, pos,
+                                   _fp(_c32(rms_att)), *ws, _fp(kc), _fp(vc), _fp(xo))
+    if rc != 0:
+        raise RuntimeError("reference q8 block failed")
     return xo, kc, vc
 
 

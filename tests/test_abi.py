@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "leap_hip_attention.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"\b(leap_hip_attention_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(leap_hip_attention_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():

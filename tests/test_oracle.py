@@ -349,6 +349,123 @@ def test_projection_pins_catch_mistakes():
     assert rel_err(no_residual, fx["x_out"]) > 1e-2
 
 
+# ---- the quantized engine: quantize, W8A8 matmul, its sub-block ------------------
+
+def _q8_fixture(path):
+    fx = _load(path)
+    dim, nh, nkv, L, sl, layer, pos, gs = (int(v) for v in fx["dims"])
+    hd = dim // nh
+    x, rms, *wf = block_inputs(rng_for(*(int(k) for k in fx["key"])), dim, nkv * hd)
+    return fx, (dim, nh, nkv, L, sl, layer, pos, gs), x, rms, wf
+
+
+def test_q8_quantize_golden():
+    fx = _load(os.path.join(GOLDEN, "q8_quantize.npz"))
+    q, sc = O.quantize(fx["x"], int(fx["gs"]))
+    assert np.array_equal(q, fx["q"]) and np.array_equal(sc, fx["s"])
+    # exact halves at scale 1 round away from zero; the zero group has scale 0
+    assert list(q[:8]) == [127, 3, -3, 1, -1, 2, 127, -127] and sc[0] == 1.0 and sc[2] == 0.0
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "q8block_*.npz"))))
+def test_q8_block_reference_golden(path):
+    fx, (dim, nh, nkv, L, sl, layer, pos, gs), x, rms, wf = _q8_fixture(path)
+    w8 = [O.quantize_weight(w, gs) for w in wf]
+    assert np.array_equal(np.concatenate([w[1] for w in w8]), fx["w_scales"]), "weight quantization differs"
+    xq, xs = O.quantize(O.rmsnorm(x, rms), gs)
+    assert np.array_equal(xq, fx["xq"]) and np.array_equal(xs, fx["xs"])
+    for w, key in zip(w8[:3], ("q_pre", "k_pre", "v_pre")):
+        assert np.array_equal(O.matmul_q8(*w, xq, xs, gs), fx[key]), f"W8A8 matmul ({key}) differs"
+    orc = O.Oracle(L, nh, nkv, dim // nh, sl)
+    orc.key_cache[layer, :pos] = fx["k_rows"]
+    orc.value_cache[layer, :pos] = fx["v_rows"]
+    got = orc.block_q8(layer, pos, x, rms, *w8, gs)
+    assert np.array_equal(got, fx["x_out"]), f"q8 block output differs: {rel_err(got, fx['x_out']):.2e}"
+    assert np.array_equal(orc.key_cache[layer, pos], fx["k_slot"])
+    assert np.array_equal(orc.value_cache[layer, pos], fx["v_slot"])
+
+
+@pytest.mark.parametrize("n,d,gs", [(64, 4, 64), (256, 7, 32), (200, 9, 64), (4096, 40, 64), (1024, 13, 128)])
+def test_q8_quantize_matmul_live_reference(n, d, gs):
+    if not O.ref_q8_available():
+        pytest.skip("quantized reference driver not built (reference sources absent)")
+    rng = rng_for(n, d, gs, 6)
+    for scale in (1e-3, 1.0, 50.0):
+        x = (scale * rng.standard_normal(n)).astype(np.float32)
+        a, b = O.quantize(x, gs), O.ref_q8_quantize(x, gs)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    # n = 200 leaves a partial group that the matmul's loop bound skips; d = 7,
+    # 9, 13 exercise the reference's row tail after its blocks of 4 rows
+    wq = rng.integers(-127, 128, (d, n), dtype=np.int8)
+    ws = (rng.random(d * n // gs) * 0.02).astype(np.float32)
+    xq, xs = O.quantize(rng.standard_normal(n), gs)
+    assert np.array_equal(O.matmul_q8(wq, ws, xq, xs, gs), O.ref_q8_matmul(wq, ws, xq, xs, gs))
+
+
+@pytest.mark.parametrize("dim,nh,nkv,L,sl,layer,pos,gs",
+                         [(512, 4, 2, 2, 50, 1, 49, 64), (256, 8, 8, 1, 9, 0, 5, 32), (1024, 8, 2, 1, 30, 0, 29, 128)])
+def test_q8_block_live_reference(dim, nh, nkv, L, sl, layer, pos, gs):
+    if not O.ref_q8_available():
+        pytest.skip("quantized reference driver not built (reference sources absent)")
+    hd = dim // nh
+    x, rms, *wf = block_inputs(rng_for(dim, pos, gs, 3), dim, nkv * hd)
+    w8 = [O.quantize_weight(w, gs) for w in wf]
+    rng = rng_for(dim, pos, gs, 4)
+    kc = normal(rng, (L, sl, nkv * hd), hd)
+    vc = normal(rng, (L, sl, nkv * hd), hd)
+    xr, kr, vr = O.ref_q8_block(dim, nh, nkv, L, sl, gs, layer, pos, x, rms, *w8, kc, vc)
+    orc = O.Oracle(L, nh, nkv, hd, sl)
+    orc.key_cache[:] = kc
+    orc.value_cache[:] = vc
+    assert np.array_equal(orc.block_q8(layer, pos, x, rms, *w8, gs), xr)
+    assert np.array_equal(orc.key_cache, kr) and np.array_equal(orc.value_cache, vr)
+
+
+def test_q8_closed_forms():
+    rng = rng_for(79)
+    gs = 64
+    x = (rng.standard_normal(gs * 8) * rng.uniform(0.01, 100, gs * 8)).astype(np.float32)
+    q, sc = O.quantize(x, gs)
+    g = x.reshape(-1, gs)
+    # the group's largest |x| maps to +-127 and sets the scale
+    assert np.all(np.abs(q.reshape(-1, gs)).max(axis=1) == 127)
+    assert np.all(np.abs(sc - np.abs(g).max(axis=1) / 127.0) <= 1e-7 * np.abs(g).max(axis=1))
+    # dequantised values lie within half a step of x
+    deq = q.reshape(-1, gs).astype(np.float64) * sc[:, None]
+    assert np.all(np.abs(deq - g) <= sc[:, None] * (0.5 + 1e-5))
+    # the matmul is the exact integer group dot products times both scales
+    d, n = 11, gs * 8
+    wq = rng.integers(-127, 128, (d, n), dtype=np.int8)
+    ws = (rng.random(d * n // gs) * 0.01).astype(np.float32)
+    idot = (wq.reshape(d, -1, gs).astype(np.int64) * q.reshape(1, -1, gs)).sum(axis=2)
+    want = (idot * ws.reshape(d, -1).astype(np.float64) * sc[None, :].astype(np.float64)).sum(axis=1)
+    assert rel_err(O.matmul_q8(wq, ws, q, sc, gs), want) < 1e-6
+    # a one-hot x quantizes to 127 at its index with scale 1/127: the
+    # product returns that column of W dequantised
+    j = 77
+    e = np.zeros(n, np.float32)
+    e[j] = 1.0
+    eq, es = O.quantize(e, gs)
+    col = wq[:, j].astype(np.float64) * ws.reshape(d, -1)[:, j // gs]
+    assert rel_err(O.matmul_q8(wq, ws, eq, es, gs), col) < 1e-6
+
+
+def test_q8_pins_catch_mistakes():
+    # ties to even in place of half away from zero, a transposed scale index
+    # and a dropped activation scale each fail a pin above
+    fx = _load(os.path.join(GOLDEN, "q8_quantize.npz"))
+    assert not np.array_equal(np.rint(fx["x"][:8] * 1.0).astype(np.int8), fx["q"][:8])
+    rng = rng_for(80)
+    gs, d, n = 64, 8, 256
+    wq = rng.integers(-127, 128, (d, n), dtype=np.int8)
+    ws = (rng.random(d * n // gs) * 0.01).astype(np.float32)
+    xq, xs = O.quantize(rng.standard_normal(n) * 5, gs)
+    good = O.matmul_q8(wq, ws, xq, xs, gs)
+    ws_t = np.ascontiguousarray(ws.reshape(d, -1).T).reshape(-1)
+    assert rel_err(O.matmul_q8(wq, ws_t, xq, xs, gs), good) > 1e-3
+    assert rel_err(O.matmul_q8(wq, ws, xq, np.ones_like(xs), gs), good) > 1e-3
+
+
 # ---- the pins catch plausible mistakes -------------------------------------------
 
 @pytest.mark.parametrize("mutant", [1, 2, 3])
