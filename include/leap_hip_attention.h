@@ -158,9 +158,8 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
  * q, k, v = W8A8 matmul (:359-652); the fp32 attention step; quantize(out);
  * x += Wo . out.  A handle holds either fp32 or int8 weights, fixed by its
  * first set call, and one group size.  dim must be 2048, 4096 or 8192 and
- * group_size a power of two with 4 <= group_size * 256 / dim <= 16 for dim
- * 2048, 2 <= ... <= 16 for 4096, 1 <= ... <= 8 for 8192 (group sizes 32 to
- * 128 or 256); others return -EINVAL. */
+ * group_size a power of two in [32, 128] (dim 2048), [32, 256] (4096) or
+ * [64, 256] (8192); others return -EINVAL. */
 int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, int group_size,
                                             const float *rms_att, const int8_t *wq, const float *wq_s,
                                             const int8_t *wk, const float *wk_s, const int8_t *wv,

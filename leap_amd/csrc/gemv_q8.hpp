@@ -10,11 +10,12 @@
 //     quantized per group, then x += Wo . that (the wo matmul and the residual
 //     after the attention block).
 //
-// Each workgroup quantizes the whole input vector itself (it is small and
-// reaches every workgroup from L2) while its weight rows are in flight: thread
-// t owns the E = n/256 consecutive values [t*E, t*E + E), so a group of gs
-// values is L = gs/E adjacent lanes, and a row's int8 load is one contiguous
-// E-byte access per thread (1 KiB per wave at n = 4096).
+// One workgroup per CU: the fp32 input vector (and the rms weight) is read,
+// normalised and quantized once per workgroup and shared through LDS, so that
+// the int8 weights, which are a quarter of the fp32 bytes per row, are not
+// outweighed by every workgroup re-reading 16-32 KiB of activations from L2.
+// A row's int8 load is one contiguous E-byte access per thread (E = n/256; 1
+// KiB per wave at n = 4096).
 //
 // Arithmetic, matched to the reference bit for bit:
 //   - group scale sx = max|v| * (1/127) (the reference's release build folds
@@ -48,7 +49,14 @@ struct Q8Args {
     int rows, n0, n1;
     int8_t *xq_out;      // [n] the quantized input as every workgroup computed it (written by workgroup 0)
     float *xs_out;       // [n / gs] its group scales
+    const int8_t *xq_in; // [n] an already quantized input (kQ8In) and its
+    const float *xs_in;  // [n / gs] group scales
 };
+
+// What the kernel's input vector is.
+constexpr int kQ8InRms = 0;   // fp32 residual stream: rmsnorm with rms_w, then quantize
+constexpr int kQ8InF32 = 1;   // fp32 vector: quantize
+constexpr int kQ8InInt8 = 2;  // already quantized (xq_in, xs_in)
 
 // Butterfly over aligned groups of L lanes (L a power of two <= 16) with the
 // DPP patterns of wave_sum; every lane of a group ends with the group's
@@ -77,6 +85,20 @@ __device__ __forceinline__ float group_max(float v)
     if constexpr (L >= 8) v = fmaxf(v, dpp_f<0x141>(v));
     if constexpr (L >= 16) v = fmaxf(v, dpp_f<0x140>(v));
     return v;
+}
+
+// Group maximum over aligned groups of W lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_max_w(float v)
+{
+    if constexpr (W <= 16) {
+        return group_max<W>(v);
+    } else {
+        v = group_max<16>(v);
+        v = fmaxf(v, __shfl_xor(v, 16));
+        if constexpr (W >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+        return v;
+    }
 }
 
 // E int8 values per thread as E/4 packed words.
@@ -108,107 +130,195 @@ __device__ __forceinline__ Q8Row<E> load_row_nt(const int8_t *p)
     return r;
 }
 
-// One workgroup of 256 threads owns rows [row0, row0 + RB).  n = 256 * E,
-// gs = L * E, NG = n / gs = 256 / L groups per row.
-template <int E, int L, int RB, bool kRms, bool kResid>
-__global__ __launch_bounds__(kGemvThreads) void q8_gemv_kernel(Q8Args a)
+constexpr int kQ8Threads = 1024;  // one workgroup per CU: 16 waves
+constexpr int kQ8Teams = kQ8Threads / kGemvThreads;
+constexpr int kQ8Waves = kQ8Threads / 64;
+
+// Rows per team the kernel can hold in registers: rpt <= q8_rpt_max<E>().
+template <int E>
+constexpr int q8_rpt_max() { return E == 32 ? 10 : 8; }
+
+// One workgroup of 1024 threads (16 waves, one per CU at the launch sizes
+// used) owns rows [row0, row0 + 4*rpt): four teams of 256 threads, team k
+// taking rows row0 + k*rpt + j, j < rpt.  In a team, thread t owns the E = n/256
+// values [t*E, t*E + E) of each of its rows, so a group of gs values is
+// L = gs/E adjacent lanes.  The input vector is read, normalised and quantized
+// once per workgroup, each thread taking E/4 consecutive values, and shared
+// through LDS; a workgroup's weight rows (4*rpt*n bytes, 96 KiB for Wq/Wk/Wv
+// at Llama-3-8B) are all in flight before anything waits.
+template <int E, int L, int kIn, bool kResid>
+__global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
 {
     constexpr int n = kGemvThreads * E;
-    constexpr int NG = kGemvThreads / L;
-    __shared__ float lds_f[NG * RB];  // (float)idot of (group, row), [group][row]
-    __shared__ float lds_c[NG * RB];  // ws * sx of (group, row)
-    __shared__ float ss_part[kGemvWaves];
+    constexpr int NG = kGemvThreads / L;   // groups per row
+    constexpr int VA = E / 4;              // input values per thread in the quantize step
+    constexpr int W = (L * E) / VA;        // threads per group in the quantize step (= 4 L)
+    constexpr int RPT = q8_rpt_max<E>();
+    constexpr int SLOTS = kQ8Teams * RPT;
+    __shared__ __align__(16) int8_t lds_xq[n];
+    __shared__ float lds_xs[NG];
+    // (float)idot and ws * sx of (row slot, group), [slot][group] with the
+    // rows padded so that the chain lanes' 128-bit reads spread over the banks
+    constexpr int NGP = NG + 4;
+    __shared__ __align__(16) float lds_f[SLOTS * NGP];
+    __shared__ __align__(16) float lds_c[SLOTS * NGP];
+    __shared__ float ss_part[kQ8Waves];
+    static_assert(2 * SLOTS * NGP * 4 + n + NG * 4 <= 64 * 1024, "LDS budget");
+    constexpr int SCL = (RPT * NG / 4 + kGemvThreads - 1) / kGemvThreads;  // scale float4s per thread
     const int tid = threadIdx.x;
-    const int g = tid / L;  // this thread's group
-    const int row0 = blockIdx.x * RB;
+    const int team = tid / kGemvThreads, tt = tid % kGemvThreads;
+    const int g = tt / L;  // this thread's group in the dot step
+    const int row0 = blockIdx.x * kQ8Teams * rpt;
+    const int rbase = row0 + team * rpt;
 
-    // 1. the weight rows and their group scales, before anything waits
-    Q8Row<E> wv[RB];
-    float sc[RB];
+    // 1. this team's group scales (rpt * NG consecutive floats, as float4s),
+    // then its weight rows, before anything waits
+    gemv_f4 scv[SCL];
 #pragma unroll
-    for (int i = 0; i < RB; i++) {
-        const int r = row0 + i < a.rows ? row0 + i : a.rows - 1;
-        wv[i] = load_row_nt<E>(a.w + (size_t)r * n + tid * E);
+    for (int i = 0; i < SCL; i++) {
+        const int e = 4 * (tt + i * kGemvThreads);  // scale index in the team's block
+        const int r = min(rbase + e / NG, a.rows - 1);
+        if (e < rpt * NG)
+            scv[i] = __builtin_nontemporal_load(reinterpret_cast<const gemv_f4 *>(a.ws + (size_t)r * NG + e % NG));
     }
+    Q8Row<E> wv[RPT];
 #pragma unroll
-    for (int i = 0; i < RB; i++) {
-        const int r = row0 + i < a.rows ? row0 + i : a.rows - 1;
-        sc[i] = __builtin_nontemporal_load(a.ws + (size_t)r * NG + g);
+    for (int j = 0; j < RPT; j++) {
+        const int r = min(rbase + j, a.rows - 1);
+        if (j < rpt) wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. the input values of this thread, rmsnorm-ed if asked
-    float v[E];
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x + tid * E);
+    if constexpr (kIn == kQ8InInt8) {
+        // 2-3. the input arrives quantized
+        if constexpr (VA == 2) {
+            reinterpret_cast<short *>(lds_xq)[tid] = reinterpret_cast<const short *>(a.xq_in)[tid];
+        } else {
 #pragma unroll
-    for (int c = 0; c < E / 4; c++) {
-        const float4 t = x4[c];
-        v[4 * c] = t.x;
-        v[4 * c + 1] = t.y;
-        v[4 * c + 2] = t.z;
-        v[4 * c + 3] = t.w;
+            for (int k = 0; k < VA / 4; k++)
+                reinterpret_cast<int *>(lds_xq)[tid * (VA / 4) + k] = reinterpret_cast<const int *>(a.xq_in)[tid * (VA / 4) + k];
+        }
+        if (tid < NG) lds_xs[tid] = a.xs_in[tid];
+    } else {
+        // 2. the input values [tid*VA, tid*VA + VA), rmsnorm-ed if asked
+        float v[VA];
+        if constexpr (VA == 2) {
+            const float2 t = reinterpret_cast<const float2 *>(a.x)[tid];
+            v[0] = t.x;
+            v[1] = t.y;
+        } else {
+#pragma unroll
+            for (int c = 0; c < VA / 4; c++) {
+                const float4 t = reinterpret_cast<const float4 *>(a.x + tid * VA)[c];
+                v[4 * c] = t.x;
+                v[4 * c + 1] = t.y;
+                v[4 * c + 2] = t.z;
+                v[4 * c + 3] = t.w;
+            }
+        }
+        if constexpr (kIn == kQ8InRms) {
+            float gw[VA];
+            if constexpr (VA == 2) {
+                const float2 t = reinterpret_cast<const float2 *>(a.rms_w)[tid];
+                gw[0] = t.x;
+                gw[1] = t.y;
+            } else {
+#pragma unroll
+                for (int c = 0; c < VA / 4; c++) {
+                    const float4 t = reinterpret_cast<const float4 *>(a.rms_w + tid * VA)[c];
+                    gw[4 * c] = t.x;
+                    gw[4 * c + 1] = t.y;
+                    gw[4 * c + 2] = t.z;
+                    gw[4 * c + 3] = t.w;
+                }
+            }
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < VA; e++) ss += v[e] * v[e];
+            ss = wave_sum(ss);
+            if (tid % 64 == 0) ss_part[tid / 64] = ss;
+            __syncthreads();
+            ss = 0.f;
+#pragma unroll
+            for (int w = 0; w < kQ8Waves; w++) ss += ss_part[w];
+            const float scale = 1.0f / sqrtf(ss / (float)n + 1e-5f);
+#pragma unroll
+            for (int e = 0; e < VA; e++) v[e] = gw[e] * (scale * v[e]);
+        }
+
+        // 3. quantize: group max over W lanes, scale, round half away from zero
+        float m = 0.f;
+#pragma unroll
+        for (int e = 0; e < VA; e++) m = fmaxf(m, fabsf(v[e]));
+        m = group_max_w<W>(m);
+        const float sx = m * (1.0f / 127.0f);
+        const float id = sx != 0.0f ? __frcp_rn(sx) : 0.0f;
+        int8_t q[VA];
+#pragma unroll
+        for (int e = 0; e < VA; e++) q[e] = (int8_t)(int)roundf(v[e] * id);
+        if constexpr (VA == 2) {
+            *reinterpret_cast<short *>(lds_xq + tid * 2) = (short)((q[0] & 0xFF) | ((q[1] & 0xFF) << 8));
+        } else {
+#pragma unroll
+            for (int k = 0; k < VA / 4; k++)
+                reinterpret_cast<int *>(lds_xq + tid * VA)[k] =
+                    (q[4 * k] & 0xFF) | ((q[4 * k + 1] & 0xFF) << 8) | ((q[4 * k + 2] & 0xFF) << 16) |
+                    ((q[4 * k + 3] & 0xFF) << 24);
+        }
+        if (tid % W == 0) lds_xs[tid / W] = sx;
     }
-    if constexpr (kRms) {
-        float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; e++) ss += v[e] * v[e];
-        ss = wave_sum(ss);
-        if (tid % 64 == 0) ss_part[tid / 64] = ss;
-        __syncthreads();
-        ss = (ss_part[0] + ss_part[1]) + (ss_part[2] + ss_part[3]);
-        const float scale = 1.0f / sqrtf(ss / (float)n + 1e-5f);
-        const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_w + tid * E);
-#pragma unroll
-        for (int c = 0; c < E / 4; c++) {
-            const float4 t = g4[c];
-            v[4 * c] = t.x * (scale * v[4 * c]);
-            v[4 * c + 1] = t.y * (scale * v[4 * c + 1]);
-            v[4 * c + 2] = t.z * (scale * v[4 * c + 2]);
-            v[4 * c + 3] = t.w * (scale * v[4 * c + 3]);
+    for (int i = 0; i < SCL; i++) {
+        const int e = 4 * (tt + i * kGemvThreads);
+        if (e < rpt * NG) {
+            float *dst = lds_c + (team * rpt + e / NG) * NGP + e % NG;
+            dst[0] = scv[i].x;
+            dst[1] = scv[i].y;
+            dst[2] = scv[i].z;
+            dst[3] = scv[i].w;
         }
     }
-
-    // 3. quantize: group max over L lanes, scale, round half away from zero
-    float m = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; e++) m = fmaxf(m, fabsf(v[e]));
-    m = group_max<L>(m);
-    const float sx = m * (1.0f / 127.0f);
-    const float id = sx != 0.0f ? __frcp_rn(sx) : 0.0f;
-    int xq[E / 4];
-#pragma unroll
-    for (int k = 0; k < E / 4; k++) {
-        int packed = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) packed |= ((int)roundf(v[4 * k + b] * id) & 0xFF) << (8 * b);
-        xq[k] = packed;
-    }
-    if (blockIdx.x == 0 && a.xq_out) {
-        int *dst = reinterpret_cast<int *>(a.xq_out + tid * E);
-#pragma unroll
-        for (int k = 0; k < E / 4; k++) dst[k] = xq[k];
-        if (tid % L == 0) a.xs_out[g] = sx;
+    __syncthreads();
+    if (kIn != kQ8InInt8 && blockIdx.x == 0 && a.xq_out) {  // the quantized input, for stage checks
+        for (int i = tid; i < n / 4; i += kQ8Threads)
+            reinterpret_cast<int *>(a.xq_out)[i] = reinterpret_cast<const int *>(lds_xq)[i];
+        for (int i = tid; i < NG; i += kQ8Threads) a.xs_out[i] = lds_xs[i];
     }
 
     // 4. exact group dot products, one (float, scale product) pair per group
+    int xq[E / 4];
 #pragma unroll
-    for (int i = 0; i < RB; i++) {
-        int d = 0;
+    for (int k = 0; k < E / 4; k++) xq[k] = reinterpret_cast<const int *>(lds_xq + tt * E)[k];
+    const float sxg = lds_xs[g];
 #pragma unroll
-        for (int k = 0; k < E / 4; k++) d = __builtin_amdgcn_sdot4(xq[k], wv[i].v[k], d, false);
-        d = group_sum_i32<L>(d);
-        if (tid % L == 0) {
-            lds_f[g * RB + i] = (float)d;
-            lds_c[g * RB + i] = sc[i] * sx;
+    for (int j = 0; j < RPT; j++) {
+        if (j < rpt) {
+            int d = 0;
+#pragma unroll
+            for (int k = 0; k < E / 4; k++) d = __builtin_amdgcn_sdot4(xq[k], wv[j].v[k], d, false);
+            d = group_sum_i32<L>(d);
+            if (tt % L == 0) {
+                const int at = (team * rpt + j) * NGP + g;
+                lds_f[at] = (float)d;
+                lds_c[at] = lds_c[at] * sxg;
+            }
         }
     }
     __syncthreads();
 
     // 5. the ordered accumulation, one lane per row
-    if (tid < RB) {
+    if (tid < kQ8Teams * rpt) {
         float val = 0.f;
-#pragma unroll 8
-        for (int j = 0; j < NG; j++) val = __builtin_fmaf(lds_f[j * RB + tid], lds_c[j * RB + tid], val);
+        const float4 *f4 = reinterpret_cast<const float4 *>(lds_f + tid * NGP);
+        const float4 *c4 = reinterpret_cast<const float4 *>(lds_c + tid * NGP);
+#pragma unroll 4
+        for (int j = 0; j < NG / 4; j++) {
+            const float4 f = f4[j], c = c4[j];
+            val = __builtin_fmaf(f.x, c.x, val);
+            val = __builtin_fmaf(f.y, c.y, val);
+            val = __builtin_fmaf(f.z, c.z, val);
+            val = __builtin_fmaf(f.w, c.w, val);
+        }
         const int r = row0 + tid;
         if (r < a.rows) {
             if constexpr (kResid) {

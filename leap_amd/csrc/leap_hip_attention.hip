@@ -150,7 +150,7 @@ int choose_chunk(const leap_hip_attention *h, int n_seq, long long total_rows, i
 
 int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
            int max_pos, long long total_rows, const float *q, const float *k, const float *v,
-           float *out, hipStream_t stream)
+           float *out, hipStream_t stream, int8_t *out_q = nullptr, float *out_qs = nullptr, int q_gs = 0)
 {
     const int hd = h->cfg.head_dim;
     KernelFn fn = pick_kernel(hd, h->group);
@@ -181,6 +181,9 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     a.grid_chunks = grid_x;
     a.n_groups = n_seq * h->cfg.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
+    a.out_q = out_q;
+    a.out_qs = out_qs;
+    a.q_gs = q_gs;
 
     // Workgroup id = ((group / 8) * grid_x + chunk) * 8 + group % 8, with
     // group = seq * n_kv_heads + kv_head: a group's chunks share one XCD.
@@ -236,34 +239,45 @@ bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
 }
 
 // Quantized projections by n = 256 * E values per row (E per thread) and
-// group size gs = L * E; RB rows per workgroup.
-using Q8Fn = void (*)(leap::Q8Args);
+// group size gs = L * E.  *rpt_max is the most rows per team the kernel holds.
+using Q8Fn = void (*)(leap::Q8Args, int);
 
-template <int E, int L>
-constexpr int q8_rows() { return E >= 32 ? 8 : 16; }
+struct Q8Kernels {
+    Q8Fn qkv;     // rmsnorm + quantize + Wq/Wk/Wv
+    Q8Fn proj;    // quantize the attention output + Wo + residual
+    Q8Fn proj_q;  // Wo + residual on an attention output the attention kernel quantized
+    int rpt_max;  // most rows per team the kernels hold
+};
 
-bool pick_q8(int dim, int gs, Q8Fn *qkv, Q8Fn *proj, int *rb)
+bool pick_q8(int dim, int gs, Q8Kernels *k)
 {
 #define LEAP_Q8(E, L)                                                                  \
     if (dim == 256 * E && gs == L * E) {                                               \
-        *qkv = leap::q8_gemv_kernel<E, L, q8_rows<E, L>(), true, false>;               \
-        *proj = leap::q8_gemv_kernel<E, L, q8_rows<E, L>(), false, true>;              \
-        *rb = q8_rows<E, L>();                                                         \
+        k->qkv = leap::q8_gemv_kernel<E, L, leap::kQ8InRms, false>;                    \
+        k->proj = leap::q8_gemv_kernel<E, L, leap::kQ8InF32, true>;                    \
+        k->proj_q = leap::q8_gemv_kernel<E, L, leap::kQ8InInt8, true>;                 \
+        k->rpt_max = leap::q8_rpt_max<E>();                                            \
         return true;                                                                   \
     }
     LEAP_Q8(8, 4) LEAP_Q8(8, 8) LEAP_Q8(8, 16)
     LEAP_Q8(16, 2) LEAP_Q8(16, 4) LEAP_Q8(16, 8) LEAP_Q8(16, 16)
-    LEAP_Q8(32, 1) LEAP_Q8(32, 2) LEAP_Q8(32, 4) LEAP_Q8(32, 8)
+    LEAP_Q8(32, 2) LEAP_Q8(32, 4) LEAP_Q8(32, 8)
 #undef LEAP_Q8
     return false;
 }
 
+// Rows per team for `rows` rows: one workgroup per CU when the rows allow it.
+int q8_rpt(int rows, int n_cu, int rpt_max)
+{
+    const int per = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
+    return std::max(1, std::min(rpt_max, per));
+}
+
 int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, hipStream_t stream)
 {
-    Q8Fn qkv, proj;
-    int rb;
-    const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs;
-    if (!pick_q8(dim, gs, &qkv, &proj, &rb))
+    Q8Kernels kq;
+    const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs, hd = h->cfg.head_dim;
+    if (!pick_q8(dim, gs, &kq))
         return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
     const size_t rows_qkv = (size_t)(dim + 2 * kv);
@@ -280,9 +294,19 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     qa.n1 = kv;
     qa.xq_out = h->q8_act;
     qa.xs_out = h->q8_act_s;
-    hipLaunchKernelGGL(qkv, dim3((unsigned)((rows_qkv + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, qa);
+    int rpt = q8_rpt((int)rows_qkv, h->n_cu, kq.rpt_max);
+    int per_wg = leap::kQ8Teams * rpt;
+    hipLaunchKernelGGL(kq.qkv, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0,
+                       stream, qa, rpt);
     HIP_TRY(h, hipGetLastError());
-    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
+    // With groups inside one head, the attention kernel quantizes its own
+    // output for the wo product (xq | aq of q8_act).
+    int8_t *aq = h->q8_act + dim;
+    float *as = h->q8_act_s + dim / gs;
+    const bool pre_q = gs <= hd;
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream, pre_q ? aq : nullptr,
+                        pre_q ? as : nullptr, gs))
+        return rc;
     leap::Q8Args pa{};
     pa.x = xb;
     pa.w = h->w8_o + (size_t)li * dim * dim;
@@ -290,9 +314,14 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     pa.out0 = x;
     pa.rows = dim;
     pa.n0 = dim;
-    pa.xq_out = h->q8_act + dim;
-    pa.xs_out = h->q8_act_s + dim / gs;
-    hipLaunchKernelGGL(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, pa);
+    pa.xq_out = aq;
+    pa.xs_out = as;
+    pa.xq_in = aq;
+    pa.xs_in = as;
+    rpt = q8_rpt(dim, h->n_cu, kq.rpt_max);
+    per_wg = leap::kQ8Teams * rpt;
+    hipLaunchKernelGGL(pre_q ? kq.proj_q : kq.proj, dim3((unsigned)((dim + per_wg - 1) / per_wg)),
+                       dim3(leap::kQ8Threads), 0, stream, pa, rpt);
     HIP_TRY(h, hipGetLastError());
     return 0;
 }
@@ -591,13 +620,12 @@ int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, in
     if (int rc = check_layer(h, layer)) return rc;
     if (!rms_att || !wq || !wq_s || !wk || !wk_s || !wv || !wv_s || !wo || !wo_s)
         return set_err(h, -EINVAL, "NULL weight");
-    Q8Fn qkv, proj;
-    int rb;
+    Q8Kernels kq;
     const int dim = h->q_dim, kv = h->kv_dim, gs = group_size;
-    if (!pick_q8(dim, gs, &qkv, &proj, &rb))
+    if (!pick_q8(dim, gs, &kq))
         return set_err(h, -EINVAL,
                        "dim %d with group size %d: the int8 projections need dim in {2048, 4096, 8192} and "
-                       "a group of 4 to 16 threads' values (2048: 32-128, 4096: 32-256, 8192: 32-256)",
+                       "a group size of 32-128 (2048), 32-256 (4096) or 64-256 (8192)",
                        dim, gs);
     if (h->w_fmt == 1) return set_err(h, -EINVAL, "this handle holds fp32 weights");
     if (h->w_fmt == 2 && gs != h->gs)

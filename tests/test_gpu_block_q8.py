@@ -109,8 +109,9 @@ def _check_stages(att, orc, layer, pos, x, got, rms, w8, gs, what):
     (4096, 32, 8, 300, 64),     # Llama-3-8B, the exporter's default group size
     (4096, 32, 8, 50, 32),
     (4096, 32, 32, 50, 256),    # multi-head, one group per 16 threads
+    (2048, 32, 4, 40, 32),      # TinyLlama, the smallest group
     (8192, 64, 8, 100, 64),     # Llama-3-70B
-    (8192, 64, 8, 20, 32),      # one thread per group
+    (8192, 64, 8, 20, 256),     # eight threads per group
     (2048, 16, 2, 1, 128),      # first token
 ])
 def test_q8_block_stages_match_oracle(hip_device, dim, nh, nkv, ctx, gs):
