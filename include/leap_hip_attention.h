@@ -154,7 +154,7 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
  * consecutive values, [d*n/group_size]: wq/wo [dim][dim], wk/wv
  * [kv_dim][dim]; rms_att [dim] fp32.  With these weights a block call runs
  * QuantizedTransformer::run_layer from its start to the attention residual
- * (QuantizedTransformer.cpp:654-936): xb = rmsnorm(x); quantize(xb) (:338-357);
+ * (QuantizedTransformer.cpp:654-945): xb = rmsnorm(x); quantize(xb) (:338-357);
  * q, k, v = W8A8 matmul (:359-652); the fp32 attention step; quantize(out);
  * x += Wo . out.  A handle holds either fp32 or int8 weights, fixed by its
  * first set call, and one group size.  dim must be 2048, 4096 or 8192 and
@@ -164,6 +164,39 @@ int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, in
                                             const float *rms_att, const int8_t *wq, const float *wq_s,
                                             const int8_t *wk, const float *wk_s, const int8_t *wv,
                                             const float *wv_s, const int8_t *wo, const float *wo_s);
+
+/* ---- Checkpoints ---------------------------------------------------------- */
+
+/* A LEAP checkpoint's header as Transformer::create reads it
+ * (TransformerFactory.cpp:59-115): magic 0x616B3432 with version 1 (fp32) or
+ * 2 (int8: shared-classifier byte and group size after the Config), weights
+ * from byte 256; or no magic (version 0, legacy fp32), the Config at byte 0
+ * and the weights from byte 28.  For fp32 files shared_classifier is
+ * vocab_size > 0 and vocab_size is made positive, as the reference does. */
+typedef struct leap_hip_attention_checkpoint {
+    int version;            /* 0, 1 or 2                                            */
+    int dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len; /* Config.h */
+    int shared_classifier;
+    int group_size;         /* version 2                                            */
+    long long header_bytes; /* where the weights start                              */
+    long long attention_bytes; /* the file must hold this many bytes for every
+                                  layer's rms_att, wq, wk, wv and wo               */
+    long long file_bytes;
+} leap_hip_attention_checkpoint;
+
+/* Parse the header of the checkpoint at `path` (host only, no GPU needed).
+ * -EIO if the file cannot be read, -EINVAL if it is not a checkpoint. */
+int leap_hip_attention_checkpoint_read(const char *path, leap_hip_attention_checkpoint *out);
+
+/* Upload, from the checkpoint at `path`, the attention weights (rms_att, wq,
+ * wk, wv, wo) of every layer the handle holds: memory-mapped, in the tensor
+ * order of memory_map_weights (FloatTransformer.cpp:947-978 for versions 0
+ * and 1, QuantizedTransformer.cpp:102-134 for version 2), through
+ * leap_hip_attention_set_layer_weights or _q8.  The checkpoint's n_layers,
+ * n_heads, n_kv_heads and head size must be the handle's (-EINVAL
+ * otherwise, and for a file shorter than attention_bytes).  This replaces the
+ * attention part of the engine's construction from a file. */
+int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path);
 
 /* ---- Extras with no counterpart in the reference ---------------------- */
 

@@ -33,8 +33,16 @@ EXPORTS = (
     "leap_hip_attention_set_split", "leap_hip_attention_kv_device_ptr",
     "leap_hip_attention_set_layer_weights", "leap_hip_attention_block",
     "leap_hip_attention_block_async", "leap_hip_attention_set_layer_weights_q8",
-    "leap_hip_attention_block_views_get",
+    "leap_hip_attention_block_views_get", "leap_hip_attention_checkpoint_read",
+    "leap_hip_attention_load_checkpoint",
 )
+
+
+class Checkpoint(ctypes.Structure):
+    """leap_hip_attention_checkpoint: a checkpoint file's header."""
+    _fields_ = [(n, ctypes.c_int) for n in ("version", "dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads",
+                                            "vocab_size", "seq_len", "shared_classifier", "group_size")] + \
+               [(n, ctypes.c_longlong) for n in ("header_bytes", "attention_bytes", "file_bytes")]
 
 
 class BlockViews(ctypes.Structure):
@@ -92,6 +100,8 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_block_async.argtypes = [H, _I, _I, _P, _P]
     L.leap_hip_attention_set_layer_weights_q8.argtypes = [H, _I, _I, _F] + [_B, _F] * 4
     L.leap_hip_attention_block_views_get.argtypes = [H, ctypes.POINTER(BlockViews)]
+    L.leap_hip_attention_checkpoint_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(Checkpoint)]
+    L.leap_hip_attention_load_checkpoint.argtypes = [H, ctypes.c_char_p]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -112,6 +122,16 @@ def _f32(a, n=None):
     if n is not None and a.size != n:
         raise ValueError(f"expected {n} floats, got {a.size}")
     return a
+
+
+def checkpoint_read(path) -> dict:
+    """The header of a LEAP checkpoint file (no GPU needed)."""
+    lib = load_library()
+    c = Checkpoint()
+    rc = lib.leap_hip_attention_checkpoint_read(os.fsencode(path), ctypes.byref(c))
+    if rc != 0:
+        raise LeapError(rc, f"{path}: {'cannot read' if rc == -errno.EIO else 'not a LEAP checkpoint'}")
+    return {n: getattr(c, n) for n, _ in Checkpoint._fields_}
 
 
 class HipAttention:
@@ -203,6 +223,10 @@ class HipAttention:
             arrs += [q, _f32(sc, rows * d // group_size)]
         args = [a.ctypes.data_as(_B) if a.dtype == np.int8 else _fp(a) for a in arrs]
         self._check(self.lib.leap_hip_attention_set_layer_weights_q8(self.h, layer, group_size, *args))
+
+    def load_checkpoint(self, path):
+        """Upload every held layer's attention weights from a checkpoint file."""
+        self._check(self.lib.leap_hip_attention_load_checkpoint(self.h, os.fsencode(path)))
 
     def block_views(self) -> dict:
         """Device addresses of the last block call's intermediates

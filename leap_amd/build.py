@@ -3,7 +3,8 @@
     python -m leap_amd.build
 
 The RoPE table TU is compiled by the host C++ compiler with the reference's
-release flags; the HIP TU by hipcc for gfx950 only.  Packed-fp32 VALU
+release flags, the checkpoint reader by the host compiler, and the HIP TU by
+hipcc for gfx950 only.  Packed-fp32 VALU
 instructions are disabled for device code (``-packed-fp32-ops``).
 """
 from __future__ import annotations
@@ -47,13 +48,16 @@ def _run(cmd):
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     rope_o = os.path.join(BUILD, "rope_table.o")
+    ckpt_o = os.path.join(BUILD, "checkpoint.o")
     hip_o = os.path.join(BUILD, "leap_hip_attention.o")
     steps = [
         ["g++", "-std=c++17", "-O3", "-march=x86-64-v3", "-ffast-math", "-fPIC", "-c",
          os.path.join(CSRC, "rope_table.cpp"), "-o", rope_o],
+        ["g++", "-std=c++17", "-O2", "-Wall", "-fPIC", "-I", INCLUDE, "-c",
+         os.path.join(CSRC, "checkpoint.cpp"), "-o", ckpt_o],
         [_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
          os.path.join(CSRC, "leap_hip_attention.hip"), "-o", hip_o],
-        [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", hip_o, rope_o],
+        [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", hip_o, rope_o, ckpt_o],
     ]
     for cmd in steps:
         if verbose:

@@ -20,6 +20,11 @@
 #include <utility>
 #include <vector>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <unistd.h>
+
+#include "checkpoint.hpp"
 #include "decode_attention.hpp"
 #include "gemv.hpp"
 #include "gemv_q8.hpp"
@@ -811,6 +816,47 @@ int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions)
                        chunk_positions);
     h->split = chunk_positions;
     return 0;
+}
+
+int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path)
+{
+    if (!h) return -EINVAL;
+    if (!path) return set_err(h, -EINVAL, "NULL path");
+    leap_hip_attention_checkpoint c;
+    if (int rc = leap_hip_attention_checkpoint_read(path, &c))
+        return set_err(h, rc, "%s: %s", path, rc == -EIO ? "cannot read" : "not a LEAP checkpoint");
+    const leap_hip_attention_config &hc = h->cfg;
+    if (c.n_layers != hc.n_layers || c.n_heads != hc.n_heads || c.n_kv_heads != hc.n_kv_heads ||
+        c.dim != hc.n_heads * hc.head_dim)
+        return set_err(h, -EINVAL, "%s: model %d layers, %d/%d heads, dim %d; the handle holds %d layers, %d/%d heads of %d",
+                       path, c.n_layers, c.n_heads, c.n_kv_heads, c.dim, hc.n_layers, hc.n_heads, hc.n_kv_heads,
+                       hc.head_dim);
+    if (c.file_bytes < c.attention_bytes)
+        return set_err(h, -EINVAL, "%s: %lld bytes, the attention weights need %lld", path, c.file_bytes,
+                       c.attention_bytes);
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return set_err(h, -EIO, "%s: cannot open", path);
+    void *map = mmap(nullptr, (size_t)c.file_bytes, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) return set_err(h, -EIO, "%s: cannot map", path);
+    const char *base = static_cast<const char *>(map);
+    int rc = 0;
+    for (int layer = hc.layer_begin; layer < hc.layer_end && rc == 0; layer++) {
+        leap::CkptLayer o;
+        size_t needed;
+        leap::ckpt_layer(c, layer, &o, &needed);
+        const auto f32 = [&](size_t off) { return reinterpret_cast<const float *>(base + off); };
+        const auto i8 = [&](size_t off) { return reinterpret_cast<const int8_t *>(base + off); };
+        if (c.version == 2)
+            rc = leap_hip_attention_set_layer_weights_q8(h, layer, c.group_size, f32(o.rms_att), i8(o.wq), f32(o.wq_s),
+                                                         i8(o.wk), f32(o.wk_s), i8(o.wv), f32(o.wv_s), i8(o.wo),
+                                                         f32(o.wo_s));
+        else
+            rc = leap_hip_attention_set_layer_weights(h, layer, f32(o.rms_att), f32(o.wq), f32(o.wk), f32(o.wv),
+                                                      f32(o.wo));
+    }
+    munmap(map, (size_t)c.file_bytes);
+    return rc;
 }
 
 int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,

@@ -75,6 +75,20 @@ public:
         check(leap_hip_attention_block(h_, layer, pos, x.data()), h_);
     }
 
+    // Every held layer's attention weights from a checkpoint file
+    // (Transformer::create's format, TransformerFactory.cpp:59-135).
+    void load_checkpoint(const std::string &path) { check(leap_hip_attention_load_checkpoint(h_, path.c_str()), h_); }
+
+    // The header of a checkpoint file.
+    static leap_hip_attention_checkpoint checkpoint_read(const std::string &path)
+    {
+        leap_hip_attention_checkpoint c{};
+        if (int rc = leap_hip_attention_checkpoint_read(path.c_str(), &c))
+            throw std::runtime_error("leap_hip_attention: cannot read checkpoint " + path + " (status " +
+                                     std::to_string(rc) + ")");
+        return c;
+    }
+
     // clear_kv_cache (FloatTransformer.cpp:74-77).
     void clear_kv_cache() { check(leap_hip_attention_clear(h_), h_); }
 

@@ -20,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle_attn.so")
 REF_SO = os.path.join(HERE, "_ref", "libleap_ref.so")
 REF_Q8_SO = os.path.join(HERE, "_ref", "libleap_ref_q8.so")
+REF_CKPT_SO = os.path.join(HERE, "_ref", "libleap_ref_ckpt.so")
 REF_SRC = "/root/reference/src/inference"
 
 _F = ctypes.POINTER(ctypes.c_float)
@@ -52,6 +53,7 @@ def _bp(a: np.ndarray):
 _lib = None
 _ref = None
 _ref_q8 = None
+_ref_ckpt = None
 
 
 def lib():
@@ -126,6 +128,31 @@ def ref_q8():
         L.leapref_q8_block.restype = _I
         _ref_q8 = L
     return _ref_q8
+
+
+def ref_ckpt_available() -> bool:
+    return os.path.isfile(REF_CKPT_SO)
+
+
+def ref_ckpt_run_layer(path, layer, pos, x, key_cache, value_cache):
+    """The reference engine built from the checkpoint at `path` by its own
+    factory runs run_layer(layer, pos, x); returns (kind, x after, key cache,
+    value cache) with kind 1 for fp32, 2 for int8."""
+    global _ref_ckpt
+    if _ref_ckpt is None:
+        if not ref_ckpt_available():
+            raise RuntimeError(f"reference driver missing: {REF_CKPT_SO}")
+        L = ctypes.CDLL(REF_CKPT_SO)
+        L.leapref_ckpt_run_layer.argtypes = [ctypes.c_char_p, _I, _I, _F, _F, _F]
+        L.leapref_ckpt_run_layer.restype = _I
+        _ref_ckpt = L
+    kc = np.array(key_cache, np.float32, copy=True)
+    vc = np.array(value_cache, np.float32, copy=True)
+    xo = np.array(x, np.float32, copy=True).reshape(-1)
+    kind = _ref_ckpt.leapref_ckpt_run_layer(os.fsencode(path), layer, pos, _fp(xo), _fp(kc), _fp(vc))
+    if kind < 0:
+        raise RuntimeError("reference checkpoint run failed")
+    return kind, xo, kc, vc
 
 
 def rope_table(seq_len: int, head_dim: int, theta: float = 500000.0):

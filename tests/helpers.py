@@ -70,3 +70,59 @@ def block_inputs(rng, dim, n_kv_dim):
     wv = normal(rng, (n_kv_dim, dim), dim)
     wo = normal(rng, (dim, dim), dim)
     return x, rms, wq, wk, wv, wo
+
+
+def write_checkpoint(path, version, dim, hidden_dim, n_heads, n_kv_heads, vocab_size, seq_len, layers,
+                     shared=True, group_size=64, rms_ffn=None, rms_final=None, emb=None, ffn=None, wcls=None):
+    """Write a LEAP checkpoint in the layout the reference's exporters write
+    and Transformer::create reads (Export.cpp:17-90 and :95-274,
+    TransformerFactory.cpp:59-135, memory_map_weights): `layers` is one
+    (rms_att, wq, wk, wv, wo) per layer, fp32 arrays for versions 0/1 and
+    (int8 values, scales) pairs for the projections in version 2.  The FFN,
+    embeddings and classifier default to zeros (the FFN then adds exactly 0
+    in run_layer).  Version 0 (legacy) stores vocab_size negated when the
+    classifier is not shared."""
+    import struct
+    L = len(layers)
+    hd = dim // n_heads
+    kv = n_kv_heads * hd
+    f32 = lambda a: np.ascontiguousarray(a, np.float32).tobytes()  # noqa: E731
+    out = bytearray()
+    cfg = [dim, hidden_dim, L, n_heads, n_kv_heads, vocab_size, seq_len]
+    if version == 0:
+        cfg[5] = vocab_size if shared else -vocab_size
+        out += struct.pack("<7i", *cfg)
+    else:
+        out += struct.pack("<Ii", 0x616B3432, version) + struct.pack("<7i", *cfg)
+        out += struct.pack("<B", 1 if shared else 0)
+        if version == 2:
+            out += struct.pack("<i", group_size)
+        out += bytes(256 - len(out))
+    z = lambda *shape: np.zeros(shape, np.float32)  # noqa: E731
+    rms_ffn = z(L, dim) + 1 if rms_ffn is None else rms_ffn
+    rms_final = z(dim) + 1 if rms_final is None else rms_final
+    emb = z(vocab_size, dim) if emb is None else emb
+    out += b"".join(f32(l[0]) for l in layers) + f32(rms_ffn) + f32(rms_final)
+    if version != 2:
+        out += f32(emb)
+        for t in range(1, 5):
+            out += b"".join(f32(l[t]) for l in layers)
+        if ffn is None:
+            out += bytes(4 * L * 3 * dim * hidden_dim)
+        else:
+            out += b"".join(f32(w) for w in ffn)
+        if not shared:
+            out += f32(z(vocab_size, dim) if wcls is None else wcls)
+    else:
+        def q8(q, sc):
+            return np.ascontiguousarray(q, np.int8).tobytes() + f32(sc)
+        out += q8(np.zeros(vocab_size * dim, np.int8), z(vocab_size * dim // group_size))
+        for t in range(1, 5):
+            out += b"".join(q8(*l[t]) for l in layers)
+        for n in (dim * hidden_dim,) * 3:  # w1, w2, w3: zero values and scales
+            out += L * (bytes(n) + bytes(4 * (n // group_size)))
+        if not shared:
+            out += q8(np.zeros(vocab_size * dim, np.int8), z(vocab_size * dim // group_size))
+    with open(path, "wb") as f:
+        f.write(out)
+    return len(out)

@@ -1,6 +1,6 @@
 """The quantized engine's attention sub-block on the GPU (rmsnorm, per-group
 int8 quantization, W8A8 q/k/v projections, attention, quantization of its
-output, W8A8 wo projection and residual: QuantizedTransformer.cpp:654-936)
+output, W8A8 wo projection and residual: QuantizedTransformer.cpp:654-945)
 against the oracle, whose every stage is bitwise equal to the reference
 (tests/test_oracle.py).
 
