@@ -21,6 +21,7 @@ struct CkptLayer {
 // Offsets of layer `layer`'s weights in a checkpoint described by `c`, and
 // the number of bytes the file must hold for every layer's attention weights
 // to be inside it.  Returns false if the sizes overflow.
-bool ckpt_layer(const leap_hip_attention_checkpoint &c, int layer, CkptLayer *out, size_t *needed);
+__attribute__((visibility("hidden"))) bool ckpt_layer(const leap_hip_attention_checkpoint &c, int layer,
+                                                     CkptLayer *out, size_t *needed);
 
 }  // namespace leap

@@ -844,7 +844,10 @@ int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path)
     for (int layer = hc.layer_begin; layer < hc.layer_end && rc == 0; layer++) {
         leap::CkptLayer o;
         size_t needed;
-        leap::ckpt_layer(c, layer, &o, &needed);
+        if (!leap::ckpt_layer(c, layer, &o, &needed)) {
+            rc = set_err(h, -EINVAL, "%s: tensor sizes overflow", path);
+            break;
+        }
         const auto f32 = [&](size_t off) { return reinterpret_cast<const float *>(base + off); };
         const auto i8 = [&](size_t off) { return reinterpret_cast<const int8_t *>(base + off); };
         if (c.version == 2)
