@@ -10,7 +10,7 @@
 // t, t + 256, ... of the input vector in registers and issues, for every row of
 // its block, the loads of the same columns, so each load instruction reads
 // 4 KiB of one row contiguously and a workgroup has RB * n * 4 bytes in flight
-// before its first FMA.  The dot products are reduced across the wave with DPP
+// before its first FMA.  The (small) input vector is loaded before the rows.  The dot products are reduced across the wave with DPP
 // and across the four waves in LDS.
 #pragma once
 
@@ -120,8 +120,8 @@ __global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
     const int n = a.dim;
     const int rows = a.dim + 2 * a.kv_dim;
     const int row0 = blockIdx.x * RB;
-    gemv_f4 wv[RB][NC];
-    issue_rows<RB, NC>(a.w, rows, row0, n, wv);
+    // The input first: load waits count outstanding loads in issue order, so
+    // the normalisation can then run while the weight rows stream.
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
     const float4 *g4 = reinterpret_cast<const float4 *>(a.rms_w);
     float4 xv[NC], gv[NC];
@@ -130,6 +130,9 @@ __global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
         xv[c] = x4[tid + kGemvThreads * c];
         gv[c] = g4[tid + kGemvThreads * c];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    gemv_f4 wv[RB][NC];
+    issue_rows<RB, NC>(a.w, rows, row0, n, wv);
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; c++) ss += dot4f(xv[c], xv[c]);
@@ -162,12 +165,13 @@ __global__ __launch_bounds__(kGemvThreads) void proj_residual_kernel(ProjArgs a)
     const int tid = threadIdx.x;
     const int n = NC * 4 * kGemvThreads;
     const int row0 = blockIdx.x * RB;
-    gemv_f4 wv[RB][NC];
-    issue_rows<RB, NC>(a.w, a.d, row0, n, wv);
     const float4 *v4 = reinterpret_cast<const float4 *>(a.xb);
     float4 xv[NC];
 #pragma unroll
     for (int c = 0; c < NC; c++) xv[c] = v4[tid + kGemvThreads * c];
+    __builtin_amdgcn_sched_barrier(0);
+    gemv_f4 wv[RB][NC];
+    issue_rows<RB, NC>(a.w, a.d, row0, n, wv);
     const float dot = finish_dots<RB, NC>(wv, xv, red);
     if (tid < RB) {
         const int r = row0 + tid;

@@ -134,26 +134,28 @@ constexpr int kQ8Threads = 1024;  // one workgroup per CU: 16 waves
 constexpr int kQ8Teams = kQ8Threads / kGemvThreads;
 constexpr int kQ8Waves = kQ8Threads / 64;
 
-// Rows per team the kernel can hold in registers: rpt <= q8_rpt_max<E>().
-template <int E>
-constexpr int q8_rpt_max() { return E == 32 ? 10 : 8; }
-
 // One workgroup of 1024 threads (16 waves, one per CU at the launch sizes
-// used) owns rows [row0, row0 + 4*rpt): four teams of 256 threads, team k
-// taking rows row0 + k*rpt + j, j < rpt.  In a team, thread t owns the E = n/256
+// used) owns rows [row0, row0 + 4*RPT): four teams of 256 threads, team k
+// taking rows row0 + k*RPT + j, j < RPT.  In a team, thread t owns the E = n/256
 // values [t*E, t*E + E) of each of its rows, so a group of gs values is
 // L = gs/E adjacent lanes.  The input vector is read, normalised and quantized
 // once per workgroup, each thread taking E/4 consecutive values, and shared
-// through LDS; a workgroup's weight rows (4*rpt*n bytes, 96 KiB for Wq/Wk/Wv
-// at Llama-3-8B) are all in flight before anything waits.
-template <int E, int L, int kIn, bool kResid>
-__global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
+// through LDS.
+//
+// Issue order: the input first, then the team's scales and weight rows
+// (4*RPT*n bytes per workgroup, 96 KiB for Wq/Wk/Wv at Llama-3-8B), all before
+// anything waits.  RPT is a compile-time count so that every load is
+// unconditional: load waits count outstanding loads in issue order, and with a
+// runtime row count the wait for the input had to assume the longest queue,
+// which made the normalisation wait for every weight row (0.8 us at
+// Llama-3-8B).  The input work now runs while the weights stream.
+template <int E, int L, int RPT, int kIn, bool kResid>
+__global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
 {
     constexpr int n = kGemvThreads * E;
     constexpr int NG = kGemvThreads / L;   // groups per row
     constexpr int VA = E / 4;              // input values per thread in the quantize step
     constexpr int W = (L * E) / VA;        // threads per group in the quantize step (= 4 L)
-    constexpr int RPT = q8_rpt_max<E>();
     constexpr int SLOTS = kQ8Teams * RPT;
     __shared__ __align__(16) int8_t lds_xq[n];
     __shared__ float lds_xs[NG];
@@ -168,40 +170,29 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
     const int tid = threadIdx.x;
     const int team = tid / kGemvThreads, tt = tid % kGemvThreads;
     const int g = tt / L;  // this thread's group in the dot step
-    const int row0 = blockIdx.x * kQ8Teams * rpt;
-    const int rbase = row0 + team * rpt;
+    const int row0 = blockIdx.x * SLOTS;
+    const int rbase = row0 + team * RPT;
 
-    // 1. this team's group scales (rpt * NG consecutive floats, as float4s),
-    // then its weight rows, before anything waits
-    gemv_f4 scv[SCL];
-#pragma unroll
-    for (int i = 0; i < SCL; i++) {
-        const int e = 4 * (tt + i * kGemvThreads);  // scale index in the team's block
-        const int r = min(rbase + e / NG, a.rows - 1);
-        if (e < rpt * NG)
-            scv[i] = __builtin_nontemporal_load(reinterpret_cast<const gemv_f4 *>(a.ws + (size_t)r * NG + e % NG));
-    }
-    Q8Row<E> wv[RPT];
-#pragma unroll
-    for (int j = 0; j < RPT; j++) {
-        const int r = min(rbase + j, a.rows - 1);
-        if (j < rpt) wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
+    // 1. the input: E/4 fp32 values (and rms weights) per thread, or the
+    // already quantized bytes and scales
+    float v[VA], gw[VA];
+    int8_t qin[VA];
+    float sin_ = 0.f;
     if constexpr (kIn == kQ8InInt8) {
-        // 2-3. the input arrives quantized
         if constexpr (VA == 2) {
-            reinterpret_cast<short *>(lds_xq)[tid] = reinterpret_cast<const short *>(a.xq_in)[tid];
+            const short t = reinterpret_cast<const short *>(a.xq_in)[tid];
+            qin[0] = (int8_t)(t & 0xFF);
+            qin[1] = (int8_t)((t >> 8) & 0xFF);
         } else {
 #pragma unroll
-            for (int k = 0; k < VA / 4; k++)
-                reinterpret_cast<int *>(lds_xq)[tid * (VA / 4) + k] = reinterpret_cast<const int *>(a.xq_in)[tid * (VA / 4) + k];
+            for (int k = 0; k < VA / 4; k++) {
+                const int t = reinterpret_cast<const int *>(a.xq_in)[tid * (VA / 4) + k];
+#pragma unroll
+                for (int b = 0; b < 4; b++) qin[4 * k + b] = (int8_t)((t >> (8 * b)) & 0xFF);
+            }
         }
-        if (tid < NG) lds_xs[tid] = a.xs_in[tid];
+        sin_ = a.xs_in[min(tid, NG - 1)];  // every lane loads: a fixed number of loads in flight
     } else {
-        // 2. the input values [tid*VA, tid*VA + VA), rmsnorm-ed if asked
-        float v[VA];
         if constexpr (VA == 2) {
             const float2 t = reinterpret_cast<const float2 *>(a.x)[tid];
             v[0] = t.x;
@@ -217,7 +208,6 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
             }
         }
         if constexpr (kIn == kQ8InRms) {
-            float gw[VA];
             if constexpr (VA == 2) {
                 const float2 t = reinterpret_cast<const float2 *>(a.rms_w)[tid];
                 gw[0] = t.x;
@@ -232,6 +222,43 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
                     gw[4 * c + 3] = t.w;
                 }
             }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. this team's group scales (RPT * NG consecutive floats, as float4s),
+    // then its weight rows
+    gemv_f4 scv[SCL];
+#pragma unroll
+    for (int i = 0; i < SCL; i++) {
+        const int e = 4 * (tt + i * kGemvThreads);  // scale index in the team's block
+        const int r = min(rbase + e / NG, a.rows - 1);
+        if (e < RPT * NG)
+            scv[i] = __builtin_nontemporal_load(reinterpret_cast<const gemv_f4 *>(a.ws + (size_t)r * NG + e % NG));
+    }
+    Q8Row<E> wv[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; j++) {
+        const int r = min(rbase + j, a.rows - 1);
+        wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. the quantized input into LDS: copied, or normalised and quantized
+    // (group max over W lanes, scale, round half away from zero)
+    if constexpr (kIn == kQ8InInt8) {
+        if constexpr (VA == 2) {
+            reinterpret_cast<short *>(lds_xq)[tid] = (short)((qin[0] & 0xFF) | ((qin[1] & 0xFF) << 8));
+        } else {
+#pragma unroll
+            for (int k = 0; k < VA / 4; k++)
+                reinterpret_cast<int *>(lds_xq)[tid * (VA / 4) + k] =
+                    (qin[4 * k] & 0xFF) | ((qin[4 * k + 1] & 0xFF) << 8) | ((qin[4 * k + 2] & 0xFF) << 16) |
+                    ((qin[4 * k + 3] & 0xFF) << 24);
+        }
+        if (tid < NG) lds_xs[tid] = sin_;
+    } else {
+        if constexpr (kIn == kQ8InRms) {
             float ss = 0.f;
 #pragma unroll
             for (int e = 0; e < VA; e++) ss += v[e] * v[e];
@@ -245,8 +272,6 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
 #pragma unroll
             for (int e = 0; e < VA; e++) v[e] = gw[e] * (scale * v[e]);
         }
-
-        // 3. quantize: group max over W lanes, scale, round half away from zero
         float m = 0.f;
 #pragma unroll
         for (int e = 0; e < VA; e++) m = fmaxf(m, fabsf(v[e]));
@@ -270,8 +295,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
 #pragma unroll
     for (int i = 0; i < SCL; i++) {
         const int e = 4 * (tt + i * kGemvThreads);
-        if (e < rpt * NG) {
-            float *dst = lds_c + (team * rpt + e / NG) * NGP + e % NG;
+        if (e < RPT * NG) {
+            float *dst = lds_c + (team * RPT + e / NG) * NGP + e % NG;
             dst[0] = scv[i].x;
             dst[1] = scv[i].y;
             dst[2] = scv[i].z;
@@ -292,22 +317,20 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a, int rpt)
     const float sxg = lds_xs[g];
 #pragma unroll
     for (int j = 0; j < RPT; j++) {
-        if (j < rpt) {
-            int d = 0;
+        int d = 0;
 #pragma unroll
-            for (int k = 0; k < E / 4; k++) d = __builtin_amdgcn_sdot4(xq[k], wv[j].v[k], d, false);
-            d = group_sum_i32<L>(d);
-            if (tt % L == 0) {
-                const int at = (team * rpt + j) * NGP + g;
-                lds_f[at] = (float)d;
-                lds_c[at] = lds_c[at] * sxg;
-            }
+        for (int k = 0; k < E / 4; k++) d = __builtin_amdgcn_sdot4(xq[k], wv[j].v[k], d, false);
+        d = group_sum_i32<L>(d);
+        if (tt % L == 0) {
+            const int at = (team * RPT + j) * NGP + g;
+            lds_f[at] = (float)d;
+            lds_c[at] = lds_c[at] * sxg;
         }
     }
     __syncthreads();
 
     // 5. the ordered accumulation, one lane per row
-    if (tid < kQ8Teams * rpt) {
+    if (tid < SLOTS) {
         float val = 0.f;
         const float4 *f4 = reinterpret_cast<const float4 *>(lds_f + tid * NGP);
         const float4 *c4 = reinterpret_cast<const float4 *>(lds_c + tid * NGP);

@@ -245,45 +245,63 @@ bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
 
 // Quantized projections by n = 256 * E values per row (E per thread) and
 // group size gs = L * E.  *rpt_max is the most rows per team the kernel holds.
-using Q8Fn = void (*)(leap::Q8Args, int);
+using Q8Fn = void (*)(leap::Q8Args);
 
-struct Q8Kernels {
-    Q8Fn qkv;     // rmsnorm + quantize + Wq/Wk/Wv
-    Q8Fn proj;    // quantize the attention output + Wo + residual
-    Q8Fn proj_q;  // Wo + residual on an attention output the attention kernel quantized
-    int rpt_max;  // most rows per team the kernels hold
+// The int8 projection kernels by (values per thread E = dim/256, lanes per
+// group L = gs/E, rows per team RPT, input kind).  RPT is compiled in (every
+// load of a thread is then unconditional); a launch takes the smallest
+// instantiated RPT that covers its rows with one workgroup per CU.
+struct Q8Entry {
+    int e, l, rpt, kind;
+    Q8Fn fn;
 };
 
-bool pick_q8(int dim, int gs, Q8Kernels *k)
+#define LEAP_Q8_K(E, L, R, K) {E, L, R, K, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms>},
+#define LEAP_Q8_QKV(E, L) LEAP_Q8_K(E, L, 2, leap::kQ8InRms) LEAP_Q8_K(E, L, 3, leap::kQ8InRms) \
+    LEAP_Q8_K(E, L, 4, leap::kQ8InRms) LEAP_Q8_K(E, L, 6, leap::kQ8InRms) LEAP_Q8_K(E, L, 8, leap::kQ8InRms) \
+    LEAP_Q8_K(E, L, 10, leap::kQ8InRms)
+#define LEAP_Q8_PROJ(E, L) LEAP_Q8_K(E, L, 2, leap::kQ8InF32) LEAP_Q8_K(E, L, 4, leap::kQ8InF32) \
+    LEAP_Q8_K(E, L, 8, leap::kQ8InF32) LEAP_Q8_K(E, L, 2, leap::kQ8InInt8) LEAP_Q8_K(E, L, 4, leap::kQ8InInt8) \
+    LEAP_Q8_K(E, L, 8, leap::kQ8InInt8)
+#define LEAP_Q8_ALL(E, L) LEAP_Q8_QKV(E, L) LEAP_Q8_PROJ(E, L)
+const Q8Entry kQ8Kernels[] = {
+    LEAP_Q8_ALL(8, 4) LEAP_Q8_ALL(8, 8) LEAP_Q8_ALL(8, 16)
+    LEAP_Q8_ALL(16, 2) LEAP_Q8_ALL(16, 4) LEAP_Q8_ALL(16, 8) LEAP_Q8_ALL(16, 16)
+    LEAP_Q8_ALL(32, 2) LEAP_Q8_ALL(32, 4) LEAP_Q8_ALL(32, 8)
+};
+#undef LEAP_Q8_ALL
+#undef LEAP_Q8_PROJ
+#undef LEAP_Q8_QKV
+#undef LEAP_Q8_K
+
+// True if (dim, gs) has int8 kernels.
+bool q8_supported(int dim, int gs)
 {
-#define LEAP_Q8(E, L)                                                                  \
-    if (dim == 256 * E && gs == L * E) {                                               \
-        k->qkv = leap::q8_gemv_kernel<E, L, leap::kQ8InRms, false>;                    \
-        k->proj = leap::q8_gemv_kernel<E, L, leap::kQ8InF32, true>;                    \
-        k->proj_q = leap::q8_gemv_kernel<E, L, leap::kQ8InInt8, true>;                 \
-        k->rpt_max = leap::q8_rpt_max<E>();                                            \
-        return true;                                                                   \
-    }
-    LEAP_Q8(8, 4) LEAP_Q8(8, 8) LEAP_Q8(8, 16)
-    LEAP_Q8(16, 2) LEAP_Q8(16, 4) LEAP_Q8(16, 8) LEAP_Q8(16, 16)
-    LEAP_Q8(32, 2) LEAP_Q8(32, 4) LEAP_Q8(32, 8)
-#undef LEAP_Q8
+    for (const Q8Entry &k : kQ8Kernels)
+        if (256 * k.e == dim && k.l * k.e == gs) return true;
     return false;
 }
 
-// Rows per team for `rows` rows: one workgroup per CU when the rows allow it.
-int q8_rpt(int rows, int n_cu, int rpt_max)
+// The kernel of `kind` for `rows` rows: the smallest RPT with 4 * RPT * n_cu
+// >= rows, else the largest; *rpt receives it.
+Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
 {
-    const int per = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
-    return std::max(1, std::min(rpt_max, per));
+    const int need = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
+    const Q8Entry *best = nullptr;
+    for (const Q8Entry &k : kQ8Kernels) {
+        if (256 * k.e != dim || k.l * k.e != gs || k.kind != kind) continue;
+        const bool covers = k.rpt >= need, best_covers = best && best->rpt >= need;
+        if (!best || (covers && (!best_covers || k.rpt < best->rpt)) || (!covers && !best_covers && k.rpt > best->rpt))
+            best = &k;
+    }
+    if (!best) return nullptr;
+    *rpt = best->rpt;
+    return best->fn;
 }
 
 int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, hipStream_t stream)
 {
-    Q8Kernels kq;
     const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs, hd = h->cfg.head_dim;
-    if (!pick_q8(dim, gs, &kq))
-        return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
     const size_t rows_qkv = (size_t)(dim + 2 * kv);
     leap::Q8Args qa{};
@@ -299,10 +317,12 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     qa.n1 = kv;
     qa.xq_out = h->q8_act;
     qa.xs_out = h->q8_act_s;
-    int rpt = q8_rpt((int)rows_qkv, h->n_cu, kq.rpt_max);
+    int rpt = 0;
+    Q8Fn fn = pick_q8(dim, gs, leap::kQ8InRms, (int)rows_qkv, h->n_cu, &rpt);
+    if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     int per_wg = leap::kQ8Teams * rpt;
-    hipLaunchKernelGGL(kq.qkv, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0,
-                       stream, qa, rpt);
+    hipLaunchKernelGGL(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream,
+                       qa);
     HIP_TRY(h, hipGetLastError());
     // With groups inside one head, the attention kernel quantizes its own
     // output for the wo product (xq | aq of q8_act).
@@ -323,10 +343,10 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     pa.xs_out = as;
     pa.xq_in = aq;
     pa.xs_in = as;
-    rpt = q8_rpt(dim, h->n_cu, kq.rpt_max);
+    fn = pick_q8(dim, gs, pre_q ? leap::kQ8InInt8 : leap::kQ8InF32, dim, h->n_cu, &rpt);
+    if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     per_wg = leap::kQ8Teams * rpt;
-    hipLaunchKernelGGL(pre_q ? kq.proj_q : kq.proj, dim3((unsigned)((dim + per_wg - 1) / per_wg)),
-                       dim3(leap::kQ8Threads), 0, stream, pa, rpt);
+    hipLaunchKernelGGL(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream, pa);
     HIP_TRY(h, hipGetLastError());
     return 0;
 }
@@ -625,9 +645,8 @@ int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, in
     if (int rc = check_layer(h, layer)) return rc;
     if (!rms_att || !wq || !wq_s || !wk || !wk_s || !wv || !wv_s || !wo || !wo_s)
         return set_err(h, -EINVAL, "NULL weight");
-    Q8Kernels kq;
     const int dim = h->q_dim, kv = h->kv_dim, gs = group_size;
-    if (!pick_q8(dim, gs, &kq))
+    if (!q8_supported(dim, gs))
         return set_err(h, -EINVAL,
                        "dim %d with group size %d: the int8 projections need dim in {2048, 4096, 8192} and "
                        "a group size of 32-128 (2048), 32-256 (4096) or 64-256 (8192)",
