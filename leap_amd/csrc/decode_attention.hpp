@@ -33,7 +33,6 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
-#include <type_traits>
 #include <stdint.h>
 
 namespace leap {
@@ -81,61 +80,7 @@ struct StepArgs {
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
-    int8_t *out_q;       // or nullptr: sequence 0's output also quantized per group of q_gs
-    float *out_qs;       // values (round half away from zero of out / scale, scale = max|out| / 127)
-    int q_gs;            // 32, 64 or 128 (a group within one head: q_gs <= HD)
 };
-
-// ---- the quantized output of the int8 engine --------------------------------
-//
-// QuantizedTransformer.cpp:338-357 applied to the attention output before the
-// wo projection: per group of q_gs consecutive values, scale = max|x| * (1/127)
-// (the reference's release build folds its division by 127 into that
-// product), q = round-half-away(x * (1/scale)), 0 for an all-zero group.  The
-// calling lane holds the 4 output values [4*col4, 4*col4 + 4) of one head; the
-// q_gs/4 lanes of a group are adjacent and active together.
-template <int QW>
-__device__ __forceinline__ float out_group_max(float m)
-{
-    const auto dpp = [](float x, auto ctrl) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), decltype(ctrl)::value,
-                                                                  0xF, 0xF, true));
-    };
-    m = fmaxf(m, dpp(m, std::integral_constant<int, 0xB1>{}));
-    m = fmaxf(m, dpp(m, std::integral_constant<int, 0x4E>{}));
-    m = fmaxf(m, dpp(m, std::integral_constant<int, 0x141>{}));
-    if constexpr (QW >= 16) m = fmaxf(m, dpp(m, std::integral_constant<int, 0x140>{}));
-    if constexpr (QW >= 32) m = fmaxf(m, __shfl_xor(m, 16));
-    return m;
-}
-
-template <int QW>
-__device__ __forceinline__ void quantize_out4(float4 o, int8_t *q_row, float *s_row, int col4)
-{
-    float m = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-    m = out_group_max<QW>(m);
-    const float sx = m * (1.0f / 127.0f);
-    const float id = sx != 0.0f ? __frcp_rn(sx) : 0.0f;
-    const int b0 = (int)roundf(o.x * id), b1 = (int)roundf(o.y * id);
-    const int b2 = (int)roundf(o.z * id), b3 = (int)roundf(o.w * id);
-    reinterpret_cast<int *>(q_row)[col4] = (b0 & 0xFF) | ((b1 & 0xFF) << 8) | ((b2 & 0xFF) << 16) | ((b3 & 0xFF) << 24);
-    if (col4 % QW == 0) s_row[col4 / QW] = sx;
-}
-
-// Quantize the output values of (head, col4) if the launch asks for it;
-// q_row/s_row point at the head's first value and first group scale.
-__device__ __forceinline__ void maybe_quantize_out(const StepArgs &a, int seq, float4 o, int head, int hd, int col4)
-{
-    if (!a.out_q || seq != 0) return;
-    int8_t *q_row = a.out_q + (size_t)head * hd;
-    float *s_row = a.out_qs + (size_t)head * hd / a.q_gs;
-    if (a.q_gs == 32)
-        quantize_out4<8>(o, q_row, s_row, col4);
-    else if (a.q_gs == 64)
-        quantize_out4<16>(o, q_row, s_row, col4);
-    else
-        quantize_out4<32>(o, q_row, s_row, col4);
-}
 
 // ---- buffer access ------------------------------------------------------------
 //
@@ -633,7 +578,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         if (single) {
             scale4(o, 1.0f / L);
             reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + ch) * HD)[cd4] = o;
-            maybe_quantize_out(a, seq, o, kvh * G + ch, HD, cd4);
         } else {
             // Partial o and (max, sum), into this XCD's L2.
             const uint32_t row = (uint32_t)ch * kRecords + (uint32_t)chunk_id;
@@ -752,7 +696,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         if (mg == 0) {
             scale4(ox, 1.0f / Lx);
             out_row[md4] = ox;
-            maybe_quantize_out(a, seq, ox, kvh * G + mh, HD, md4);
         }
         return;
     }
@@ -776,7 +719,6 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     if (mg == 0) {
         scale4(ox, 1.0f / Lx);
         out_row[md4] = ox;
-        maybe_quantize_out(a, seq, ox, kvh * G + mh, HD, md4);
     }
 }
 

@@ -49,14 +49,11 @@ struct Q8Args {
     int rows, n0, n1;
     int8_t *xq_out;      // [n] the quantized input as every workgroup computed it (written by workgroup 0)
     float *xs_out;       // [n / gs] its group scales
-    const int8_t *xq_in; // [n] an already quantized input (kQ8In) and its
-    const float *xs_in;  // [n / gs] group scales
 };
 
 // What the kernel's input vector is.
 constexpr int kQ8InRms = 0;   // fp32 residual stream: rmsnorm with rms_w, then quantize
-constexpr int kQ8InF32 = 1;   // fp32 vector: quantize
-constexpr int kQ8InInt8 = 2;  // already quantized (xq_in, xs_in)
+constexpr int kQ8InF32 = 1;   // fp32 vector (the attention output): quantize
 
 // Butterfly over aligned groups of L lanes (L a power of two <= 16) with the
 // DPP patterns of wave_sum; every lane of a group ends with the group's
@@ -173,54 +170,35 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
     const int row0 = blockIdx.x * SLOTS;
     const int rbase = row0 + team * RPT;
 
-    // 1. the input: E/4 fp32 values (and rms weights) per thread, or the
-    // already quantized bytes and scales
+    // 1. the input: E/4 fp32 values (and rms weights) per thread
     float v[VA], gw[VA];
-    int8_t qin[VA];
-    float sin_ = 0.f;
-    if constexpr (kIn == kQ8InInt8) {
-        if constexpr (VA == 2) {
-            const short t = reinterpret_cast<const short *>(a.xq_in)[tid];
-            qin[0] = (int8_t)(t & 0xFF);
-            qin[1] = (int8_t)((t >> 8) & 0xFF);
-        } else {
-#pragma unroll
-            for (int k = 0; k < VA / 4; k++) {
-                const int t = reinterpret_cast<const int *>(a.xq_in)[tid * (VA / 4) + k];
-#pragma unroll
-                for (int b = 0; b < 4; b++) qin[4 * k + b] = (int8_t)((t >> (8 * b)) & 0xFF);
-            }
-        }
-        sin_ = a.xs_in[min(tid, NG - 1)];  // every lane loads: a fixed number of loads in flight
+    if constexpr (VA == 2) {
+        const float2 t = reinterpret_cast<const float2 *>(a.x)[tid];
+        v[0] = t.x;
+        v[1] = t.y;
     } else {
+#pragma unroll
+        for (int c = 0; c < VA / 4; c++) {
+            const float4 t = reinterpret_cast<const float4 *>(a.x + tid * VA)[c];
+            v[4 * c] = t.x;
+            v[4 * c + 1] = t.y;
+            v[4 * c + 2] = t.z;
+            v[4 * c + 3] = t.w;
+        }
+    }
+    if constexpr (kIn == kQ8InRms) {
         if constexpr (VA == 2) {
-            const float2 t = reinterpret_cast<const float2 *>(a.x)[tid];
-            v[0] = t.x;
-            v[1] = t.y;
+            const float2 t = reinterpret_cast<const float2 *>(a.rms_w)[tid];
+            gw[0] = t.x;
+            gw[1] = t.y;
         } else {
 #pragma unroll
             for (int c = 0; c < VA / 4; c++) {
-                const float4 t = reinterpret_cast<const float4 *>(a.x + tid * VA)[c];
-                v[4 * c] = t.x;
-                v[4 * c + 1] = t.y;
-                v[4 * c + 2] = t.z;
-                v[4 * c + 3] = t.w;
-            }
-        }
-        if constexpr (kIn == kQ8InRms) {
-            if constexpr (VA == 2) {
-                const float2 t = reinterpret_cast<const float2 *>(a.rms_w)[tid];
-                gw[0] = t.x;
-                gw[1] = t.y;
-            } else {
-#pragma unroll
-                for (int c = 0; c < VA / 4; c++) {
-                    const float4 t = reinterpret_cast<const float4 *>(a.rms_w + tid * VA)[c];
-                    gw[4 * c] = t.x;
-                    gw[4 * c + 1] = t.y;
-                    gw[4 * c + 2] = t.z;
-                    gw[4 * c + 3] = t.w;
-                }
+                const float4 t = reinterpret_cast<const float4 *>(a.rms_w + tid * VA)[c];
+                gw[4 * c] = t.x;
+                gw[4 * c + 1] = t.y;
+                gw[4 * c + 2] = t.z;
+                gw[4 * c + 3] = t.w;
             }
         }
     }
@@ -244,54 +222,41 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. the quantized input into LDS: copied, or normalised and quantized
-    // (group max over W lanes, scale, round half away from zero)
-    if constexpr (kIn == kQ8InInt8) {
-        if constexpr (VA == 2) {
-            reinterpret_cast<short *>(lds_xq)[tid] = (short)((qin[0] & 0xFF) | ((qin[1] & 0xFF) << 8));
-        } else {
+    // 3. the input normalised (if asked) and quantized into LDS: group max
+    // over W lanes, scale, round half away from zero
+    if constexpr (kIn == kQ8InRms) {
+        float ss = 0.f;
 #pragma unroll
-            for (int k = 0; k < VA / 4; k++)
-                reinterpret_cast<int *>(lds_xq)[tid * (VA / 4) + k] =
-                    (qin[4 * k] & 0xFF) | ((qin[4 * k + 1] & 0xFF) << 8) | ((qin[4 * k + 2] & 0xFF) << 16) |
-                    ((qin[4 * k + 3] & 0xFF) << 24);
-        }
-        if (tid < NG) lds_xs[tid] = sin_;
-    } else {
-        if constexpr (kIn == kQ8InRms) {
-            float ss = 0.f;
+        for (int e = 0; e < VA; e++) ss += v[e] * v[e];
+        ss = wave_sum(ss);
+        if (tid % 64 == 0) ss_part[tid / 64] = ss;
+        __syncthreads();
+        ss = 0.f;
 #pragma unroll
-            for (int e = 0; e < VA; e++) ss += v[e] * v[e];
-            ss = wave_sum(ss);
-            if (tid % 64 == 0) ss_part[tid / 64] = ss;
-            __syncthreads();
-            ss = 0.f;
+        for (int w = 0; w < kQ8Waves; w++) ss += ss_part[w];
+        const float scale = 1.0f / sqrtf(ss / (float)n + 1e-5f);
 #pragma unroll
-            for (int w = 0; w < kQ8Waves; w++) ss += ss_part[w];
-            const float scale = 1.0f / sqrtf(ss / (float)n + 1e-5f);
-#pragma unroll
-            for (int e = 0; e < VA; e++) v[e] = gw[e] * (scale * v[e]);
-        }
-        float m = 0.f;
-#pragma unroll
-        for (int e = 0; e < VA; e++) m = fmaxf(m, fabsf(v[e]));
-        m = group_max_w<W>(m);
-        const float sx = m * (1.0f / 127.0f);
-        const float id = sx != 0.0f ? __frcp_rn(sx) : 0.0f;
-        int8_t q[VA];
-#pragma unroll
-        for (int e = 0; e < VA; e++) q[e] = (int8_t)(int)roundf(v[e] * id);
-        if constexpr (VA == 2) {
-            *reinterpret_cast<short *>(lds_xq + tid * 2) = (short)((q[0] & 0xFF) | ((q[1] & 0xFF) << 8));
-        } else {
-#pragma unroll
-            for (int k = 0; k < VA / 4; k++)
-                reinterpret_cast<int *>(lds_xq + tid * VA)[k] =
-                    (q[4 * k] & 0xFF) | ((q[4 * k + 1] & 0xFF) << 8) | ((q[4 * k + 2] & 0xFF) << 16) |
-                    ((q[4 * k + 3] & 0xFF) << 24);
-        }
-        if (tid % W == 0) lds_xs[tid / W] = sx;
+        for (int e = 0; e < VA; e++) v[e] = gw[e] * (scale * v[e]);
     }
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < VA; e++) m = fmaxf(m, fabsf(v[e]));
+    m = group_max_w<W>(m);
+    const float sx = m * (1.0f / 127.0f);
+    const float id = sx != 0.0f ? __frcp_rn(sx) : 0.0f;
+    int8_t q[VA];
+#pragma unroll
+    for (int e = 0; e < VA; e++) q[e] = (int8_t)(int)roundf(v[e] * id);
+    if constexpr (VA == 2) {
+        *reinterpret_cast<short *>(lds_xq + tid * 2) = (short)((q[0] & 0xFF) | ((q[1] & 0xFF) << 8));
+    } else {
+#pragma unroll
+        for (int k = 0; k < VA / 4; k++)
+            reinterpret_cast<int *>(lds_xq + tid * VA)[k] =
+                (q[4 * k] & 0xFF) | ((q[4 * k + 1] & 0xFF) << 8) | ((q[4 * k + 2] & 0xFF) << 16) |
+                ((q[4 * k + 3] & 0xFF) << 24);
+    }
+    if (tid % W == 0) lds_xs[tid / W] = sx;
 #pragma unroll
     for (int i = 0; i < SCL; i++) {
         const int e = 4 * (tt + i * kGemvThreads);
@@ -304,7 +269,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
         }
     }
     __syncthreads();
-    if (kIn != kQ8InInt8 && blockIdx.x == 0 && a.xq_out) {  // the quantized input, for stage checks
+    if (blockIdx.x == 0 && a.xq_out) {  // the quantized input, for stage checks
         for (int i = tid; i < n / 4; i += kQ8Threads)
             reinterpret_cast<int *>(a.xq_out)[i] = reinterpret_cast<const int *>(lds_xq)[i];
         for (int i = tid; i < NG; i += kQ8Threads) a.xs_out[i] = lds_xs[i];

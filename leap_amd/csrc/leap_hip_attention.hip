@@ -155,7 +155,7 @@ int choose_chunk(const leap_hip_attention *h, int n_seq, long long total_rows, i
 
 int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
            int max_pos, long long total_rows, const float *q, const float *k, const float *v,
-           float *out, hipStream_t stream, int8_t *out_q = nullptr, float *out_qs = nullptr, int q_gs = 0)
+           float *out, hipStream_t stream)
 {
     const int hd = h->cfg.head_dim;
     KernelFn fn = pick_kernel(hd, h->group);
@@ -186,9 +186,6 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     a.grid_chunks = grid_x;
     a.n_groups = n_seq * h->cfg.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
-    a.out_q = out_q;
-    a.out_qs = out_qs;
-    a.q_gs = q_gs;
 
     // Workgroup id = ((group / 8) * grid_x + chunk) * 8 + group % 8, with
     // group = seq * n_kv_heads + kv_head: a group's chunks share one XCD.
@@ -261,8 +258,7 @@ struct Q8Entry {
     LEAP_Q8_K(E, L, 4, leap::kQ8InRms) LEAP_Q8_K(E, L, 6, leap::kQ8InRms) LEAP_Q8_K(E, L, 8, leap::kQ8InRms) \
     LEAP_Q8_K(E, L, 10, leap::kQ8InRms)
 #define LEAP_Q8_PROJ(E, L) LEAP_Q8_K(E, L, 2, leap::kQ8InF32) LEAP_Q8_K(E, L, 4, leap::kQ8InF32) \
-    LEAP_Q8_K(E, L, 8, leap::kQ8InF32) LEAP_Q8_K(E, L, 2, leap::kQ8InInt8) LEAP_Q8_K(E, L, 4, leap::kQ8InInt8) \
-    LEAP_Q8_K(E, L, 8, leap::kQ8InInt8)
+    LEAP_Q8_K(E, L, 8, leap::kQ8InF32)
 #define LEAP_Q8_ALL(E, L) LEAP_Q8_QKV(E, L) LEAP_Q8_PROJ(E, L)
 const Q8Entry kQ8Kernels[] = {
     LEAP_Q8_ALL(8, 4) LEAP_Q8_ALL(8, 8) LEAP_Q8_ALL(8, 16)
@@ -301,7 +297,7 @@ Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
 
 int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, hipStream_t stream)
 {
-    const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs, hd = h->cfg.head_dim;
+    const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs;
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
     const size_t rows_qkv = (size_t)(dim + 2 * kv);
     leap::Q8Args qa{};
@@ -324,14 +320,9 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     hipLaunchKernelGGL(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream,
                        qa);
     HIP_TRY(h, hipGetLastError());
-    // With groups inside one head, the attention kernel quantizes its own
-    // output for the wo product (xq | aq of q8_act).
     int8_t *aq = h->q8_act + dim;
     float *as = h->q8_act_s + dim / gs;
-    const bool pre_q = gs <= hd;
-    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream, pre_q ? aq : nullptr,
-                        pre_q ? as : nullptr, gs))
-        return rc;
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
     leap::Q8Args pa{};
     pa.x = xb;
     pa.w = h->w8_o + (size_t)li * dim * dim;
@@ -341,9 +332,7 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     pa.n0 = dim;
     pa.xq_out = aq;
     pa.xs_out = as;
-    pa.xq_in = aq;
-    pa.xs_in = as;
-    fn = pick_q8(dim, gs, pre_q ? leap::kQ8InInt8 : leap::kQ8InF32, dim, h->n_cu, &rpt);
+    fn = pick_q8(dim, gs, leap::kQ8InF32, dim, h->n_cu, &rpt);
     if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     per_wg = leap::kQ8Teams * rpt;
     hipLaunchKernelGGL(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream, pa);
