@@ -8,7 +8,7 @@
 // synthetic q/k/v in place of the projections (the GEMVs are outside the
 // path) and calls the shim for the attention block of every layer.
 //
-//   engine_demo n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block]
+//   engine_demo n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block | ckpt PATH]
 //
 // writes, per (token, layer) in decode order, q|k|v|xb as raw fp32 to
 // out_dir/trace.bin so a checker can replay the same steps on a CPU
@@ -16,7 +16,10 @@
 // attention residual (:394-683) instead: the program generates each layer's
 // rms_att, wq, wk, wv, wo (written to out_dir/weights.bin in that order, per
 // layer), feeds the residual stream x from layer to layer and token to token,
-// and writes x before and after every (token, layer) to trace.bin.
+// and writes x before and after every (token, layer) to trace.bin.  With
+// `ckpt PATH` the weights come from a LEAP checkpoint file instead (fp32 or
+// int8, through the shim's loader; the file's Config must match the
+// arguments), and the same trace is written.
 // Exit status: 0 success, 2 bad usage, 3 shim error.
 #include <cstdio>
 #include <cmath>
@@ -53,8 +56,10 @@ struct RunState {  // the attention-facing part of FloatRunState
 int main(int argc, char **argv)
 {
     const bool block = argc == 9 && std::string(argv[8]) == "block";
-    if (argc != 8 && !block) {
-        std::fprintf(stderr, "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block]\n",
+    const bool ckpt = argc == 10 && std::string(argv[8]) == "ckpt";
+    if (argc != 8 && !block && !ckpt) {
+        std::fprintf(stderr,
+                     "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block | ckpt PATH]\n",
                      argv[0]);
         return 2;
     }
@@ -79,6 +84,24 @@ int main(int argc, char **argv)
         if (!f) {
             std::fprintf(stderr, "cannot write %s/trace.bin\n", out_dir.c_str());
             return 2;
+        }
+        if (ckpt) {  // the weights of every layer from a checkpoint file
+            const auto info = leap::HipAttention::checkpoint_read(argv[9]);
+            std::printf("engine_demo: checkpoint version %d, %d layers, dim %d\n", info.version, info.n_layers,
+                        info.dim);
+            attn.load_checkpoint(argv[9]);
+            std::vector<float> x(dim);
+            for (float &e : x) e = rng.next(1.0f);
+            for (int pos = 0; pos < n_tokens; pos++) {
+                for (int l = 0; l < n_layers; l++) {
+                    std::fwrite(x.data(), 4, x.size(), f);
+                    attn.block(l, pos, x);
+                    std::fwrite(x.data(), 4, x.size(), f);
+                }
+            }
+            std::fclose(f);
+            std::printf("engine_demo: %d tokens x %d layers done (checkpoint)\n", n_tokens, n_layers);
+            return 0;
         }
         if (block) {
             std::FILE *wf = std::fopen((out_dir + "/weights.bin").c_str(), "wb");

@@ -66,6 +66,28 @@ public:
               h_);
     }
 
+    // The int8 engine's weights of one held layer: each projection as the
+    // reference's QuantizedTensor (QuantizedTransformer.h:9-12), int8 values
+    // [d][n] and one scale per group of group_size values.
+    struct QTensor {
+        std::span<const int8_t> q;
+        std::span<const float> s;
+    };
+    void set_layer_weights_q8(int layer, int group_size, std::span<const float> rms_att, QTensor wq, QTensor wk,
+                              QTensor wv, QTensor wo)
+    {
+        const size_t dim = (size_t)q_dim_, kv = (size_t)kv_dim_;
+        const auto ok = [&](const QTensor &t, size_t rows) {
+            return group_size > 0 && t.q.size() == rows * dim && t.s.size() == rows * dim / (size_t)group_size;
+        };
+        if (rms_att.size() != dim || !ok(wq, dim) || !ok(wk, kv) || !ok(wv, kv) || !ok(wo, dim))
+            throw std::invalid_argument("HipAttention::set_layer_weights_q8: weight sizes do not match the model");
+        check(leap_hip_attention_set_layer_weights_q8(h_, layer, group_size, rms_att.data(), wq.q.data(),
+                                                      wq.s.data(), wk.q.data(), wk.s.data(), wv.q.data(),
+                                                      wv.s.data(), wo.q.data(), wo.s.data()),
+              h_);
+    }
+
     // run_layer(l, pos, x) from its start to the attention residual
     // (FloatTransformer.cpp:394-683): x += Wo . attention(Wq/Wk/Wv . rmsnorm(x)).
     void block(int layer, int pos, std::span<float> x)

@@ -73,3 +73,34 @@ def test_engine_demo_block_matches_oracle(tmp_path, hip_device):
             x_in, x_out = trace[pos, layer]
             want = orc.block(layer, pos, x_in, *weights[layer])
             assert_close(x_out - x_in, want - x_in, what=f"token {pos} layer {layer}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("version", [1, 2])
+def test_engine_demo_checkpoint_matches_oracle(tmp_path, hip_device, version):
+    """The engine loop with its weights loaded from a checkpoint file (fp32 or
+    int8) through the C++ wrapper: 12 tokens x 2 layers against the oracle's
+    chain on the same tensors."""
+    from tests.helpers import block_inputs, rng_for, write_checkpoint
+    L, nh, nkv, hd, seq_len, n_tok, gs = 2, 16, 4, 128, 16, 12, 64
+    dim, kv = nh * hd, nkv * hd
+    layers = []
+    for layer in range(L):
+        _, rms, *wf = block_inputs(rng_for(dim, layer, version, 31), dim, kv)
+        layers.append((rms, *(O.quantize_weight(w, gs) for w in wf)) if version == 2 else (rms, *wf))
+    path = tmp_path / "m.bin"
+    write_checkpoint(path, version, dim, 64, nh, nkv, 4, seq_len, layers, group_size=gs)
+    r = subprocess.run([_demo(), str(L), str(nh), str(nkv), str(hd), str(seq_len), str(n_tok), str(tmp_path),
+                        "ckpt", str(path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    trace = np.fromfile(tmp_path / "trace.bin", dtype=np.float32).reshape(n_tok, L, 2, dim)
+    orc = O.Oracle(L, nh, nkv, hd, seq_len)
+    for pos in range(n_tok):
+        for layer in range(L):
+            x_in, x_out = trace[pos, layer]
+            if version == 2:
+                want = orc.block_q8(layer, pos, x_in, *layers[layer], gs)
+                assert_close(x_out - x_in, want - x_in, rel=1e-3, what=f"int8 token {pos} layer {layer}")
+            else:
+                want = orc.block(layer, pos, x_in, *layers[layer])
+                assert_close(x_out - x_in, want - x_in, what=f"token {pos} layer {layer}")

@@ -112,6 +112,8 @@ def _check_stages(att, orc, layer, pos, x, got, rms, w8, gs, what):
     (2048, 32, 4, 40, 32),      # TinyLlama, the smallest group
     (8192, 64, 8, 100, 64),     # Llama-3-70B
     (8192, 64, 8, 20, 256),     # eight threads per group
+    (8192, 64, 8, 33, 128),     # four threads per group
+    (4096, 32, 8, 65, 128),     # eight threads per group at Llama-3-8B
     (2048, 16, 2, 1, 128),      # first token
 ])
 def test_q8_block_stages_match_oracle(hip_device, dim, nh, nkv, ctx, gs):
