@@ -27,6 +27,12 @@ engine's sub-block: int8 weights with one float scale per group of 64 values
 (the reference exporter's default), the activations quantized per group on the
 device; their bytes count the int8 weights and their scales.
 
+For the batch-1 workloads the line also carries `host_pointer`: the same bytes
+per layer-step over the time of the synchronous host-pointer entry point
+(`leap_hip_attention_step`, or `leap_hip_attention_block`), which copies its
+inputs and result over PCIe and waits for them in every call.  It is reported
+beside `value`, never as `value`.
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
 """
 from __future__ import annotations
@@ -206,6 +212,52 @@ def cpu_baseline(att, workload, Ts, n_layers_sample: int, budget_s: float):
     }
 
 
+def host_pointer_rate(att, L, pos, bytes_layer, is_block, sweeps):
+    """The synchronous host-pointer entry point the engine calls, timed on the host clock.
+
+    Each call copies its inputs from pageable host memory, runs the launches
+    and copies the result back before it returns, as `leap_hip_attention_step`
+    (or `leap_hip_attention_block`) does for an engine whose buffers live in
+    std::vector.  Buffers are allocated once; the call is made through ctypes
+    without the binding's per-call copies.
+    """
+    from leap_amd.attention import _fp
+    rng = np.random.default_rng(SEED)
+    lib, h = att.lib, att.h
+    if is_block:
+        x = (rng.standard_normal(att.q_dim) * 0.1).astype(np.float32)
+        xp = _fp(x)
+
+        def sweep():
+            for l in range(L):
+                rc = lib.leap_hip_attention_block(h, l, pos, xp)
+                if rc:
+                    raise RuntimeError(f"leap_hip_attention_block returned {rc}")
+        entry, host_bytes = "leap_hip_attention_block", 8 * att.q_dim
+    else:
+        bufs = [(rng.standard_normal(n) / np.sqrt(att.head_dim)).astype(np.float32)
+                for n in (att.q_dim, att.kv_dim, att.kv_dim)]
+        out = np.empty(att.q_dim, np.float32)
+        ptrs = [_fp(b) for b in bufs] + [_fp(out)]
+
+        def sweep():
+            for l in range(L):
+                rc = lib.leap_hip_attention_step(h, l, pos, *ptrs)
+                if rc:
+                    raise RuntimeError(f"leap_hip_attention_step returned {rc}")
+        entry, host_bytes = "leap_hip_attention_step", 4 * (2 * att.q_dim + 2 * att.kv_dim)
+    sweep()
+    t0 = time.perf_counter()
+    for _ in range(sweeps):
+        sweep()
+    us = (time.perf_counter() - t0) * 1e6 / (sweeps * L)
+    return {"entry": entry, "value": round(bytes_layer / (us * 1e-6) / 1e9, 2), "unit": "GB/s",
+            "us_per_layer_step": round(us, 3), "host_bytes_per_layer_step": host_bytes,
+            "sweeps": sweeps,
+            "note": "pageable host buffers: copies in, launches, copy out and a stream "
+                    "synchronisation in every call (PCIe-inclusive; not the device-resident value)"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -375,6 +427,9 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if batch == 1:
+        result["host_pointer"] = host_pointer_rate(att, L, pos, bytes_layer, is_block,
+                                                   sweeps=max(1, min(steps, 20)))
     if not args.no_cpu:
         try:
             if is_block:

@@ -198,6 +198,52 @@ int leap_hip_attention_checkpoint_read(const char *path, leap_hip_attention_chec
  * attention part of the engine's construction from a file. */
 int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path);
 
+/* ---- Stage hand-off (pipeline across nodes) -------------------------------- */
+
+/* A pipeline packet is the reference's PacketHeader {int32 pos; int32 flags}
+ * (Transformer.h:25-31) followed by the dim fp32 values of the residual
+ * stream x, dim = n_heads * head_dim: the master sends it after its layers
+ * (FloatTransformer.cpp:775-788) and each worker reads it, runs its layers
+ * and forwards it (:925-939).  A packet that starts with the uint16
+ * CONTROL_MAGIC 0xC0DE is a control message of the same size (Transport.h:
+ * 41-47, worker_loop :871-923); control messages belong to the transport's
+ * control plane and are not handled here. */
+#define LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES 8
+#define LEAP_HIP_ATTENTION_FLAG_NO_REPLY 0
+#define LEAP_HIP_ATTENTION_FLAG_NEED_REPLY 1
+#define LEAP_HIP_ATTENTION_CONTROL_MAGIC 0xC0DE
+
+/* Read a packet's header (host only, no GPU): returns 0 for a data packet
+ * with *pos and *flags set, 1 for a control packet, -EINVAL when `bytes` is
+ * not 8 + 4*dim. */
+int leap_hip_attention_packet_header(const void *packet, size_t bytes, int dim, int *pos,
+                                     int *flags);
+
+/* worker_loop's receive side (FloatTransformer.cpp:925-926): copy a data
+ * packet's dim floats into the device residual stream `x` and return its
+ * header in *pos and *flags, ready for leap_hip_attention_block_async(h,
+ * layer, *pos, x, stream) over the held layers.  Returns 1, copying
+ * nothing, for a control packet; -EINVAL for a wrong size or a pos outside
+ * [0, seq_len).  With a NULL stream the copy runs on the handle's own
+ * stream and has finished when the call returns; that stream does not wait
+ * for work the caller enqueued on other streams, so x must not be in use
+ * there.  Otherwise the copy is enqueued on `stream` and `packet` must stay
+ * unchanged until the stream has passed it (pinned host memory makes it a
+ * DMA; the reference's worker receives into a std::vector, which is
+ * pageable). */
+int leap_hip_attention_packet_upload(leap_hip_attention *h, const void *packet, size_t bytes,
+                                     float *x, int *pos, int *flags, void *stream);
+
+/* The send side (FloatTransformer.cpp:775-778 and 937-938): write the header
+ * {pos, flags} and copy the device residual stream `x` after it, into the
+ * host buffer `packet` of 8 + 4*dim bytes.  With a NULL stream the packet is
+ * complete when the call returns (the copy runs on the handle's own stream:
+ * finish the work that writes x on other streams first); otherwise its
+ * values are, once `stream` has passed the copy.  A worker forwards the packet unless it is the tail
+ * and flags is not FLAG_NEED_REPLY (:937). */
+int leap_hip_attention_packet_download(leap_hip_attention *h, const float *x, int pos, int flags,
+                                       void *packet, size_t bytes, void *stream);
+
 /* ---- Extras with no counterpart in the reference ---------------------- */
 
 /* Fill every cache row of every held sequence and layer with seeded

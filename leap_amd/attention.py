@@ -34,8 +34,12 @@ EXPORTS = (
     "leap_hip_attention_set_layer_weights", "leap_hip_attention_block",
     "leap_hip_attention_block_async", "leap_hip_attention_set_layer_weights_q8",
     "leap_hip_attention_block_views_get", "leap_hip_attention_checkpoint_read",
-    "leap_hip_attention_load_checkpoint",
+    "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
+    "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
 )
+
+PACKET_HEADER_BYTES = 8
+FLAG_NO_REPLY, FLAG_NEED_REPLY = 0, 1
 
 
 class Checkpoint(ctypes.Structure):
@@ -102,6 +106,10 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_block_views_get.argtypes = [H, ctypes.POINTER(BlockViews)]
     L.leap_hip_attention_checkpoint_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(Checkpoint)]
     L.leap_hip_attention_load_checkpoint.argtypes = [H, ctypes.c_char_p]
+    _IP = ctypes.POINTER(_I)
+    L.leap_hip_attention_packet_header.argtypes = [ctypes.c_char_p, ctypes.c_size_t, _I, _IP, _IP]
+    L.leap_hip_attention_packet_upload.argtypes = [H, ctypes.c_char_p, ctypes.c_size_t, _P, _IP, _IP, _P]
+    L.leap_hip_attention_packet_download.argtypes = [H, _P, _I, _I, _P, ctypes.c_size_t, _P]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -132,6 +140,16 @@ def checkpoint_read(path) -> dict:
     if rc != 0:
         raise LeapError(rc, f"{path}: {'cannot read' if rc == -errno.EIO else 'not a LEAP checkpoint'}")
     return {n: getattr(c, n) for n, _ in Checkpoint._fields_}
+
+
+def packet_header(packet: bytes, dim):
+    """(pos, flags) of a stage packet, or None for a control packet (no GPU needed)."""
+    pos, flags = _I(), _I()
+    rc = load_library().leap_hip_attention_packet_header(packet, len(packet), dim, ctypes.byref(pos),
+                                                         ctypes.byref(flags))
+    if rc < 0:
+        raise LeapError(rc, f"packet of {len(packet)} bytes is not 8 + 4*{dim}")
+    return None if rc == 1 else (pos.value, flags.value)
 
 
 class HipAttention:
@@ -243,6 +261,24 @@ class HipAttention:
 
     def block_async(self, layer, pos, x_ptr, stream=0):
         self._check(self.lib.leap_hip_attention_block_async(self.h, layer, pos, x_ptr, stream))
+
+    # -- stage hand-off -----------------------------------------------------
+    def packet_upload(self, packet: bytes, x_ptr, stream=0):
+        """Copy a data packet's x to device memory at x_ptr; returns (pos, flags),
+        or None for a control packet.  stream 0: synchronous."""
+        pos, flags = _I(), _I()
+        rc = self.lib.leap_hip_attention_packet_upload(self.h, packet, len(packet), x_ptr, ctypes.byref(pos),
+                                                       ctypes.byref(flags), stream)
+        if rc == 1:
+            return None
+        self._check(rc)
+        return pos.value, flags.value
+
+    def packet_download(self, x_ptr, pos, flags) -> bytes:
+        """The packet {pos, flags} + x (device memory at x_ptr), synchronously."""
+        buf = ctypes.create_string_buffer(PACKET_HEADER_BYTES + 4 * self.q_dim)
+        self._check(self.lib.leap_hip_attention_packet_download(self.h, x_ptr, pos, flags, buf, len(buf), None))
+        return buf.raw
 
     # -- cache management ---------------------------------------------------
     def clear(self):

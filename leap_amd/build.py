@@ -22,6 +22,7 @@ BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libleap_hip_attention.so")
 DEMO = os.path.join(PKG, "host", "engine_demo")
 ARCH = "gfx950"
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
@@ -67,8 +68,10 @@ def build(verbose: bool = False) -> str:
     # the C++20 engine-side wrapper and demo layer loop, linked against the
     # library in place
     demo = ["g++", "-std=c++20", "-O2", "-Wall", "-I", INCLUDE, "-I", os.path.join(PKG, "host"),
+            "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
             os.path.join(PKG, "host", "engine_demo.cpp"), "-o", DEMO + ".tmp", "-L", PKG,
-            "-lleap_hip_attention", "-Wl,-rpath,$ORIGIN/.."]
+            "-lleap_hip_attention", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+            "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
     if verbose:
         print(" ".join(demo))
     _run(demo)

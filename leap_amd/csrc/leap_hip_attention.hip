@@ -723,6 +723,62 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
     return 0;
 }
 
+// ---- stage hand-off -------------------------------------------------------
+
+int leap_hip_attention_packet_header(const void *packet, size_t bytes, int dim, int *pos, int *flags)
+{
+    constexpr size_t kHead = LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES;
+    if (!packet || dim <= 0 || bytes != kHead + sizeof(float) * (size_t)dim) return -EINVAL;
+    uint16_t magic;
+    std::memcpy(&magic, packet, sizeof magic);
+    if (magic == LEAP_HIP_ATTENTION_CONTROL_MAGIC) return 1;
+    int32_t head[2];
+    std::memcpy(head, packet, sizeof head);
+    if (pos) *pos = head[0];
+    if (flags) *flags = head[1];
+    return 0;
+}
+
+int leap_hip_attention_packet_upload(leap_hip_attention *h, const void *packet, size_t bytes, float *x,
+                                     int *pos, int *flags, void *stream)
+{
+    if (!h) return -EINVAL;
+    if (!packet || !x || !pos || !flags) return set_err(h, -EINVAL, "NULL buffer");
+    int p, f;
+    const int rc = leap_hip_attention_packet_header(packet, bytes, h->q_dim, &p, &f);
+    if (rc < 0) return set_err(h, rc, "packet of %zu bytes, expected %zu", bytes,
+                               LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES + sizeof(float) * (size_t)h->q_dim);
+    if (rc == 1) return 1;
+    if (p < 0 || p >= h->cfg.seq_len) return set_err(h, -EINVAL, "packet pos %d outside [0, %d)", p, h->cfg.seq_len);
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    const char *src = static_cast<const char *>(packet) + LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES;
+    HIP_TRY(h, hipMemcpyAsync(x, src, sizeof(float) * (size_t)h->q_dim, hipMemcpyHostToDevice, s));
+    if (!stream) HIP_TRY(h, hipStreamSynchronize(s));
+    *pos = p;
+    *flags = f;
+    return 0;
+}
+
+int leap_hip_attention_packet_download(leap_hip_attention *h, const float *x, int pos, int flags, void *packet,
+                                       size_t bytes, void *stream)
+{
+    if (!h) return -EINVAL;
+    if (!packet || !x) return set_err(h, -EINVAL, "NULL buffer");
+    constexpr size_t kHead = LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES;
+    if (bytes != kHead + sizeof(float) * (size_t)h->q_dim)
+        return set_err(h, -EINVAL, "packet of %zu bytes, expected %zu", bytes, kHead + sizeof(float) * (size_t)h->q_dim);
+    if (pos < 0 || pos >= h->cfg.seq_len) return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    hipStream_t s = stream ? (hipStream_t)stream : h->stream;
+    const int32_t head[2] = {pos, flags};
+    std::memcpy(packet, head, sizeof head);
+    HIP_TRY(h, hipMemcpyAsync(static_cast<char *>(packet) + kHead, x, sizeof(float) * (size_t)h->q_dim,
+                              hipMemcpyDeviceToHost, s));
+    if (!stream) HIP_TRY(h, hipStreamSynchronize(s));
+    return 0;
+}
+
 int leap_hip_attention_clear(leap_hip_attention *h)
 {
     if (!h) return -EINVAL;

@@ -20,12 +20,31 @@
 // `ckpt PATH` the weights come from a LEAP checkpoint file instead (fp32 or
 // int8, through the shim's loader; the file's Config must match the
 // arguments), and the same trace is written.
+//
+//   engine_demo ... out_dir pipeline PATH SPLIT
+//
+// runs the same checkpoint as a two-node pipeline in one process: a master
+// handle holds layers [0, SPLIT) and a tail worker handle [SPLIT, n_layers),
+// each keeping its residual stream in device memory.  Per token the master
+// runs its layers and sends the packet {pos, flags} + x (FloatTransformer.cpp:
+// 775-778); the worker receives it (:925-926), runs its layers and forwards
+// it back only when a reply is wanted (:937-939), and the master takes x
+// from the reply (:785-788).  Every third token is sent without asking for a
+// reply, as a prompt token is.  Per token the trace holds x before the
+// master's layers, the packet sent, an int32 that says whether the worker
+// forwarded, the packet it forwarded and the master's x after the reply
+// (zeros where nothing was forwarded).
 // Exit status: 0 success, 2 bad usage, 3 shim error.
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
 #include <cstdio>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
+#include <algorithm>
 #include <exception>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -51,15 +70,83 @@ struct RunState {  // the attention-facing part of FloatRunState
     std::vector<float> q, k, v, xb;
 };
 
+// Device memory the engine owns for its residual stream.
+struct DeviceFloats {
+    float *p = nullptr;
+    explicit DeviceFloats(size_t n)
+    {
+        if (hipMalloc((void **)&p, n * sizeof(float)) != hipSuccess) throw std::runtime_error("hipMalloc failed");
+    }
+    ~DeviceFloats() { (void)hipFree(p); }
+    DeviceFloats(const DeviceFloats &) = delete;
+    DeviceFloats &operator=(const DeviceFloats &) = delete;
+};
+
+void hip_ok(hipError_t e, const char *what)
+{
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// The two-node pipeline of the checkpoint at `path` (see the header).
+int run_pipeline(int n_layers, int n_heads, int n_kv, int head_dim, int seq_len, int n_tokens, const std::string &path,
+                 int split, std::FILE *f)
+{
+    leap::HipAttention master({n_layers, 0, split, n_heads, n_kv, head_dim, seq_len});
+    leap::HipAttention worker({n_layers, split, n_layers, n_heads, n_kv, head_dim, seq_len});
+    master.load_checkpoint(path);
+    worker.load_checkpoint(path);
+    const int dim = n_heads * head_dim;
+    DeviceFloats xm(dim), xw(dim);
+    hipStream_t s;
+    hip_ok(hipStreamCreate(&s), "hipStreamCreate");
+    std::vector<std::byte> sent(master.packet_bytes()), reply(master.packet_bytes());
+    std::vector<float> x(dim), back(dim);
+    Rng rng{0x4C454150};
+    for (float &e : x) e = rng.next(1.0f);
+    for (int pos = 0; pos < n_tokens; pos++) {
+        const int flags = pos % 3 == 2 ? LEAP_HIP_ATTENTION_FLAG_NO_REPLY : LEAP_HIP_ATTENTION_FLAG_NEED_REPLY;
+        std::fwrite(x.data(), 4, x.size(), f);
+        hip_ok(hipMemcpyAsync(xm.p, x.data(), dim * sizeof(float), hipMemcpyHostToDevice, s), "copy x");
+        for (int l = 0; l < split; l++) master.block_async(l, pos, xm.p, s);  // forward :768-770
+        master.download_packet(xm.p, {pos, flags}, sent, s);
+        hip_ok(hipStreamSynchronize(s), "sync");  // the transport sends the packet
+        std::fwrite(sent.data(), 1, sent.size(), f);
+        // the worker (worker_loop :869-939)
+        const auto hd = worker.upload_packet(sent, xw.p, s);
+        if (!hd) throw std::runtime_error("a data packet was read as a control packet");
+        for (int l = split; l < n_layers; l++) worker.block_async(l, hd->pos, xw.p, s);
+        const int32_t fwd = leap::HipAttention::forwards(true, hd->flags) ? 1 : 0;
+        std::fill(reply.begin(), reply.end(), std::byte{0});
+        std::fill(back.begin(), back.end(), 0.0f);
+        if (fwd) {
+            worker.download_packet(xw.p, *hd, reply, s);
+            hip_ok(hipStreamSynchronize(s), "sync");
+            // the master receives the reply and takes its x (:785-788)
+            if (!master.upload_packet(reply, xm.p, s)) throw std::runtime_error("reply read as a control packet");
+            hip_ok(hipMemcpyAsync(back.data(), xm.p, dim * sizeof(float), hipMemcpyDeviceToHost, s), "copy x");
+        }
+        hip_ok(hipStreamSynchronize(s), "sync");
+        std::fwrite(&fwd, 4, 1, f);
+        std::fwrite(reply.data(), 1, reply.size(), f);
+        std::fwrite(back.data(), 4, back.size(), f);
+        for (float &e : x) e = rng.next(1.0f);  // the next token's embedding row
+    }
+    hip_ok(hipStreamDestroy(s), "hipStreamDestroy");
+    std::printf("engine_demo: %d tokens through a %d + %d layer pipeline\n", n_tokens, split, n_layers - split);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv)
 {
     const bool block = argc == 9 && std::string(argv[8]) == "block";
     const bool ckpt = argc == 10 && std::string(argv[8]) == "ckpt";
-    if (argc != 8 && !block && !ckpt) {
+    const bool pipeline = argc == 11 && std::string(argv[8]) == "pipeline";
+    if (argc != 8 && !block && !ckpt && !pipeline) {
         std::fprintf(stderr,
-                     "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir [block | ckpt PATH]\n",
+                     "usage: %s n_layers n_heads n_kv_heads head_dim seq_len n_tokens out_dir "
+                     "[block | ckpt PATH | pipeline PATH SPLIT]\n",
                      argv[0]);
         return 2;
     }
@@ -71,6 +158,21 @@ int main(int argc, char **argv)
         return 2;
     }
     try {
+        if (pipeline) {
+            const int split = std::atoi(argv[10]);
+            if (split <= 0 || split >= n_layers) {
+                std::fprintf(stderr, "SPLIT must be in [1, n_layers)\n");
+                return 2;
+            }
+            std::FILE *f = std::fopen((out_dir + "/trace.bin").c_str(), "wb");
+            if (!f) {
+                std::fprintf(stderr, "cannot write %s/trace.bin\n", out_dir.c_str());
+                return 2;
+            }
+            const int rc = run_pipeline(n_layers, n_heads, n_kv, head_dim, seq_len, n_tokens, argv[9], split, f);
+            std::fclose(f);
+            return rc;
+        }
         leap::HipAttention attn({n_layers, 0, n_layers, n_heads, n_kv, head_dim, seq_len});
         RunState s;
         const int dim = n_heads * head_dim, kv_dim = n_kv * head_dim;

@@ -8,7 +8,9 @@
 // one call.
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
+#include <optional>
 #include <span>
 #include <stdexcept>
 #include <string>
@@ -96,6 +98,45 @@ public:
             throw std::invalid_argument("HipAttention::block: x must hold dim floats");
         check(leap_hip_attention_block(h_, layer, pos, x.data()), h_);
     }
+
+    // The same with x in device memory (16-byte aligned), enqueued on `stream`.
+    void block_async(int layer, int pos, float *x_dev, void *stream)
+    {
+        check(leap_hip_attention_block_async(h_, layer, pos, x_dev, stream), h_);
+    }
+
+    // ---- the stage hand-off of a pipeline (FloatTransformer.cpp:775-788, 925-939)
+
+    // PacketHeader (Transformer.h:25-28).
+    struct PacketHeader {
+        int pos, flags;
+    };
+    size_t packet_bytes() const { return LEAP_HIP_ATTENTION_PACKET_HEADER_BYTES + sizeof(float) * (size_t)q_dim_; }
+
+    // A received packet's x into the device residual stream x_dev; its header,
+    // or nothing for a control packet (the transport's business).  Enqueued on
+    // `stream`; a null stream waits for the copy.
+    std::optional<PacketHeader> upload_packet(std::span<const std::byte> packet, float *x_dev, void *stream = nullptr)
+    {
+        PacketHeader hd{};
+        const int rc = leap_hip_attention_packet_upload(h_, packet.data(), packet.size(), x_dev, &hd.pos, &hd.flags,
+                                                        stream);
+        if (rc == 1) return std::nullopt;
+        check(rc, h_);
+        return hd;
+    }
+
+    // The packet {header, x_dev} for the next stage; its values are in place
+    // once `stream` has passed the copy (at return for a null stream).
+    void download_packet(const float *x_dev, PacketHeader hd, std::span<std::byte> packet, void *stream = nullptr)
+    {
+        check(leap_hip_attention_packet_download(h_, x_dev, hd.pos, hd.flags, packet.data(), packet.size(), stream),
+              h_);
+    }
+
+    // worker_loop forwards after its layers unless it is the tail and no
+    // reply is wanted (FloatTransformer.cpp:937).
+    static bool forwards(bool is_tail, int flags) { return !is_tail || flags == LEAP_HIP_ATTENTION_FLAG_NEED_REPLY; }
 
     // Every held layer's attention weights from a checkpoint file
     // (Transformer::create's format, TransformerFactory.cpp:59-135).

@@ -4,7 +4,9 @@ ctypes bindings for the CPU restatement (``liboracle_attn.so``, built from
 ``attn_oracle.c``) and for the driver around the reference's own code
 (``_ref/libleap_ref.so``, built from ``ref_harness.cpp`` plus the reference's
 ``src/inference/FloatTransformer.cpp``; ``_ref/libleap_ref_q8.so``, built from
-``ref_harness_q8.cpp`` plus ``src/inference/QuantizedTransformer.cpp``).  Only the tests, the smoke check and
+``ref_harness_q8.cpp`` plus ``src/inference/QuantizedTransformer.cpp``;
+``_ref/libleap_ref_ckpt.so``, built from ``ref_harness_ckpt.cpp`` plus the
+reference's checkpoint factory and both engines).  Only the tests, the smoke check and
 the CPU-baseline leg of the benchmark import this module; the product package
 ``leap_amd`` never does.
 """
@@ -138,6 +140,16 @@ def ref_ckpt_run_layer(path, layer, pos, x, key_cache, value_cache):
     """The reference engine built from the checkpoint at `path` by its own
     factory runs run_layer(layer, pos, x); returns (kind, x after, key cache,
     value cache) with kind 1 for fp32, 2 for int8."""
+    kc = np.array(key_cache, np.float32, copy=True)
+    vc = np.array(value_cache, np.float32, copy=True)
+    xo = np.array(x, np.float32, copy=True).reshape(-1)
+    kind = _ckpt_lib().leapref_ckpt_run_layer(os.fsencode(path), layer, pos, _fp(xo), _fp(kc), _fp(vc))
+    if kind < 0:
+        raise RuntimeError("reference checkpoint run failed")
+    return kind, xo, kc, vc
+
+
+def _ckpt_lib():
     global _ref_ckpt
     if _ref_ckpt is None:
         if not ref_ckpt_available():
@@ -145,14 +157,80 @@ def ref_ckpt_run_layer(path, layer, pos, x, key_cache, value_cache):
         L = ctypes.CDLL(REF_CKPT_SO)
         L.leapref_ckpt_run_layer.argtypes = [ctypes.c_char_p, _I, _I, _F, _F, _F]
         L.leapref_ckpt_run_layer.restype = _I
+        _U = ctypes.c_char_p
+        _IP = ctypes.POINTER(_I)
+        L.leapref_ckpt_master.argtypes = [ctypes.c_char_p, _I, _I, _IP, _IP, _IP, _U, _I, ctypes.c_void_p]
+        L.leapref_ckpt_master.restype = _I
+        L.leapref_ckpt_worker.argtypes = [ctypes.c_char_p, _I, _I, _I, _I, _U, ctypes.c_void_p]
+        L.leapref_ckpt_worker.restype = _I
         _ref_ckpt = L
-    kc = np.array(key_cache, np.float32, copy=True)
-    vc = np.array(value_cache, np.float32, copy=True)
-    xo = np.array(x, np.float32, copy=True).reshape(-1)
-    kind = _ref_ckpt.leapref_ckpt_run_layer(os.fsencode(path), layer, pos, _fp(xo), _fp(kc), _fp(vc))
-    if kind < 0:
-        raise RuntimeError("reference checkpoint run failed")
-    return kind, xo, kc, vc
+    return _ref_ckpt
+
+
+def _ints(a):
+    a = np.ascontiguousarray(a, np.int32)
+    return a, a.ctypes.data_as(ctypes.POINTER(_I))
+
+
+def ref_ckpt_master(path, split, dim, tokens, pos, flags, replies=()):
+    """The reference engine from `path` as a pipeline master that runs layers
+    [0, split): forward(tokens[i], pos[i], flags[i]) for each i, with the
+    packets that the forwards asking for a reply receive given in `replies`.
+    Returns the packets it sent (bytes each)."""
+    n = len(tokens)
+    nb = PACKET_HEADER_BYTES + 4 * dim
+    t, tp = _ints(tokens)
+    p, pp = _ints(pos)
+    f, fp = _ints(flags)
+    rep = b"".join(replies)
+    out = ctypes.create_string_buffer(n * nb)
+    got = _ckpt_lib().leapref_ckpt_master(os.fsencode(path), split, n, tp, pp, fp, rep, len(replies), out)
+    if got < 0:
+        raise RuntimeError("reference master run failed")
+    return [out.raw[i * nb:(i + 1) * nb] for i in range(got)]
+
+
+def ref_ckpt_worker(path, split, end, is_tail, dim, packets):
+    """The reference engine from `path` as a pipeline worker for layers
+    [split, end), fed `packets` (bytes each) through worker_loop; returns
+    the packets it forwarded."""
+    nb = PACKET_HEADER_BYTES + 4 * dim
+    out = ctypes.create_string_buffer(max(1, len(packets)) * nb)
+    got = _ckpt_lib().leapref_ckpt_worker(os.fsencode(path), split, end, int(is_tail), len(packets),
+                                          b"".join(packets), out)
+    if got < 0:
+        raise RuntimeError("reference worker run failed")
+    return [out.raw[i * nb:(i + 1) * nb] for i in range(got)]
+
+
+# ---- the stage hand-off (a restatement, pinned against the two above) ------------
+
+PACKET_HEADER_BYTES = 8
+FLAG_NO_REPLY, FLAG_NEED_REPLY = 0, 1
+CONTROL_MAGIC = 0xC0DE
+
+
+def packet_pack(pos, flags, x) -> bytes:
+    """PacketHeader {int pos; int flags} then the dim floats of x, as forward
+    sends them (Transformer.h:25-28; FloatTransformer.cpp:775-778)."""
+    import struct
+    return struct.pack("<ii", pos, flags) + np.ascontiguousarray(x, np.float32).tobytes()
+
+
+def packet_unpack(packet: bytes, dim):
+    """(pos, flags, x) of a data packet, as worker_loop reads it
+    (FloatTransformer.cpp:925-926)."""
+    import struct
+    assert len(packet) == PACKET_HEADER_BYTES + 4 * dim
+    pos, flags = struct.unpack_from("<ii", packet)
+    return pos, flags, np.frombuffer(packet, np.float32, dim, PACKET_HEADER_BYTES).copy()
+
+
+def packet_forwards(is_tail, flags) -> bool:
+    """Whether a worker forwards the packet after its layers: every stage but
+    the tail does, and the tail only when a reply is wanted
+    (FloatTransformer.cpp:937-939)."""
+    return (not is_tail) or flags == FLAG_NEED_REPLY
 
 
 def rope_table(seq_len: int, head_dim: int, theta: float = 500000.0):
