@@ -43,8 +43,14 @@ struct leap_hip_attention {
     float *ws_o = nullptr;
     float2 *ws_ml = nullptr;
     int *counters = nullptr;
-    int *pos_dev = nullptr;
-    float *q_dev = nullptr, *k_dev = nullptr, *v_dev = nullptr, *out_dev = nullptr;
+    // The host-pointer entry points stage their inputs through one pinned
+    // host buffer and one device region (q rows | k rows | v rows | pos, packed
+    // for the call's n_seq), so that each call makes one DMA in and one out.
+    char *in_dev = nullptr;
+    char *in_host = nullptr;  // pinned, the same size
+    float *out_host = nullptr;// pinned, max_batch * q_dim
+    size_t in_bytes = 0;
+    float *out_dev = nullptr;
     // attention sub-block: per-layer weights (allocated on the first
     // set_layer_weights) and the block's own q, k, v, attention-out buffers
     float *w_qkv = nullptr;   // [n_local][dim + 2*kv_dim][dim]
@@ -461,11 +467,12 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters;
     CREATE_TRY(hipMalloc(&h->counters, n_ctr * sizeof(int)));
     CREATE_TRY(hipMemsetAsync(h->counters, 0, n_ctr * sizeof(int), h->stream));
-    CREATE_TRY(hipMalloc(&h->pos_dev, (size_t)c.max_batch * sizeof(int)));
-    CREATE_TRY(hipMalloc(&h->q_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
+    h->in_bytes = (size_t)c.max_batch * ((h->q_dim + 2 * h->kv_dim) * sizeof(float) + sizeof(int));
+    CREATE_TRY(hipMalloc(&h->in_dev, h->in_bytes));
+    CREATE_TRY(hipHostMalloc((void **)&h->in_host, h->in_bytes, hipHostMallocDefault));
+    CREATE_TRY(hipHostMalloc((void **)&h->out_host, (size_t)c.max_batch * h->q_dim * sizeof(float),
+                             hipHostMallocDefault));
     CREATE_TRY(hipMalloc(&h->out_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
-    CREATE_TRY(hipMalloc(&h->k_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
-    CREATE_TRY(hipMalloc(&h->v_dev, (size_t)c.max_batch * h->kv_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->blk, (size_t)(3 * h->q_dim + 2 * h->kv_dim) * sizeof(float)));
     h->w_set.assign(h->n_local, 0);
     CREATE_TRY(hipStreamSynchronize(h->stream));
@@ -478,11 +485,13 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
 {
     if (!h) return 0;
     if (h->stream) (void)hipStreamSynchronize(h->stream);
-    void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->pos_dev,
-                    h->q_dev,   h->k_dev,   h->v_dev, h->out_dev, h->blk,  h->w_qkv,    h->w_o,
-                    h->w_rms,   h->w8_qkv,  h->s8_qkv, h->w8_o, h->s8_o, h->q8_act, h->q8_act_s};
+    void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->in_dev,
+                    h->out_dev, h->blk,     h->w_qkv, h->w_o,   h->w_rms, h->w8_qkv,   h->s8_qkv,
+                    h->w8_o,    h->s8_o,    h->q8_act, h->q8_act_s};
     for (void *p : bufs)
         if (p) (void)hipFree(p);
+    for (void *p : {(void *)h->in_host, (void *)h->out_host})
+        if (p) (void)hipHostFree(p);
     if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
     return 0;
@@ -517,14 +526,18 @@ int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const flo
     if (!q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     hipStream_t s = h->stream;
-    HIP_TRY(h, hipMemcpyAsync(h->q_dev, q, h->q_dim * sizeof(float), hipMemcpyHostToDevice, s));
-    HIP_TRY(h, hipMemcpyAsync(h->k_dev, k_new, h->kv_dim * sizeof(float), hipMemcpyHostToDevice, s));
-    HIP_TRY(h, hipMemcpyAsync(h->v_dev, v_new, h->kv_dim * sizeof(float), hipMemcpyHostToDevice, s));
-    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, h->q_dev, h->k_dev, h->v_dev,
+    const size_t qb = h->q_dim * sizeof(float), kb = h->kv_dim * sizeof(float);
+    std::memcpy(h->in_host, q, qb);
+    std::memcpy(h->in_host + qb, k_new, kb);
+    std::memcpy(h->in_host + qb + kb, v_new, kb);
+    HIP_TRY(h, hipMemcpyAsync(h->in_dev, h->in_host, qb + 2 * kb, hipMemcpyHostToDevice, s));
+    const float *qd = reinterpret_cast<const float *>(h->in_dev);
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, qd, qd + h->q_dim, qd + h->q_dim + h->kv_dim,
                         h->out_dev, s))
         return rc;
-    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, h->q_dim * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipMemcpyAsync(h->out_host, h->out_dev, qb, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    std::memcpy(out, h->out_host, qb);
     return 0;
 }
 
@@ -570,19 +583,20 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
     }
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     hipStream_t s = h->stream;
-    HIP_TRY(h, hipMemcpyAsync(h->pos_dev, pos, n_seq * sizeof(int), hipMemcpyHostToDevice, s));
-    HIP_TRY(h, hipMemcpyAsync(h->q_dev, q, (size_t)n_seq * h->q_dim * sizeof(float),
-                              hipMemcpyHostToDevice, s));
-    HIP_TRY(h, hipMemcpyAsync(h->k_dev, k_new, (size_t)n_seq * h->kv_dim * sizeof(float),
-                              hipMemcpyHostToDevice, s));
-    HIP_TRY(h, hipMemcpyAsync(h->v_dev, v_new, (size_t)n_seq * h->kv_dim * sizeof(float),
-                              hipMemcpyHostToDevice, s));
-    if (int rc = launch(h, layer, n_seq, h->pos_dev, 0, max_pos, rows, h->q_dev, h->k_dev,
-                        h->v_dev, h->out_dev, s))
-        return rc;
-    HIP_TRY(h, hipMemcpyAsync(out, h->out_dev, (size_t)n_seq * h->q_dim * sizeof(float),
-                              hipMemcpyDeviceToHost, s));
+    // packed for n_seq: q rows | k rows | v rows | pos (every offset a multiple of 256 bytes but pos's)
+    const size_t qb = (size_t)n_seq * h->q_dim * sizeof(float), kb = (size_t)n_seq * h->kv_dim * sizeof(float);
+    std::memcpy(h->in_host, q, qb);
+    std::memcpy(h->in_host + qb, k_new, kb);
+    std::memcpy(h->in_host + qb + kb, v_new, kb);
+    std::memcpy(h->in_host + qb + 2 * kb, pos, n_seq * sizeof(int));
+    HIP_TRY(h, hipMemcpyAsync(h->in_dev, h->in_host, qb + 2 * kb + n_seq * sizeof(int), hipMemcpyHostToDevice, s));
+    const float *qd = reinterpret_cast<const float *>(h->in_dev);
+    const float *kd = qd + (size_t)n_seq * h->q_dim, *vd = kd + (size_t)n_seq * h->kv_dim;
+    const int *pd = reinterpret_cast<const int *>(h->in_dev + qb + 2 * kb);
+    if (int rc = launch(h, layer, n_seq, pd, 0, max_pos, rows, qd, kd, vd, h->out_dev, s)) return rc;
+    HIP_TRY(h, hipMemcpyAsync(h->out_host, h->out_dev, qb, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    std::memcpy(out, h->out_host, qb);
     return 0;
 }
 
@@ -716,10 +730,13 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     hipStream_t s = h->stream;
     float *xd = h->blk + 2 * h->q_dim + 2 * h->kv_dim;
-    HIP_TRY(h, hipMemcpyAsync(xd, x, (size_t)h->q_dim * sizeof(float), hipMemcpyHostToDevice, s));
+    const size_t xb = (size_t)h->q_dim * sizeof(float);
+    std::memcpy(h->out_host, x, xb);  // through pinned memory: one DMA each way
+    HIP_TRY(h, hipMemcpyAsync(xd, h->out_host, xb, hipMemcpyHostToDevice, s));
     if (int rc = launch_block(h, layer, pos, xd, s)) return rc;
-    HIP_TRY(h, hipMemcpyAsync(x, xd, (size_t)h->q_dim * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(h, hipMemcpyAsync(h->out_host, xd, xb, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
+    std::memcpy(x, h->out_host, xb);
     return 0;
 }
 
