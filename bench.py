@@ -70,13 +70,14 @@ WORKLOADS = {
     "llama3.1-8b-ctx131072": (32, 32, 8, 128, 500000.0, 1, 131072, 4),
     "llama3-8b-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 5),
     "llama3-8b-q8-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 6),
+    "llama3.2-3b-ctx4096": (28, 24, 8, 128, 500000.0, 1, 4096, 7),
 }
 BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096", "llama3-8b-q8-block-ctx4096"}
 Q8_WORKLOADS = {"llama3-8b-q8-block-ctx4096"}
 DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3-8b-batch64-ragged": 10, "llama3-70b-stage20-batch16": 10,
                  "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30,
-                 "llama3-8b-q8-block-ctx4096": 50}
+                 "llama3-8b-q8-block-ctx4096": 50, "llama3.2-3b-ctx4096": 100}
 
 
 def algorithmic_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:

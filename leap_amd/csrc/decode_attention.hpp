@@ -248,11 +248,13 @@ struct Shape {
     static constexpr int VS = R / RPV;                     // V load sets per sub-tile
     static constexpr int ROWS = NW * R;                    // positions per workgroup pass
     static constexpr int D4 = HD / 4;                      // float4 per head row
-    static constexpr int MG = THREADS / (G * D4);          // merge: chunk lanes per head
+    // merge: heads padded to a power of two (3 -> 4), chunk lanes per head
+    static constexpr int GM = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+    static constexpr int MG = THREADS / (GM * D4);
     static_assert(HD % 32 == 0, "head_dim vs K slices");
     static_assert(R % 8 == 0 && R % RPV == 0, "sub-tile shape");
     static_assert(G <= 8, "q heads per KV head");
-    static_assert(MG >= 1 && THREADS % (G * D4) == 0, "merge layout");
+    static_assert(MG >= 1 && THREADS % (GM * D4) == 0, "merge layout");
 };
 
 template <int HD, int G, int NW>
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 {
     using S = Shape<HD, G, NW>;
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
-    constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, MG = S::MG;
+    constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, GM = S::GM, MG = S::MG;
 
     // id = ((group / 8) * grid_chunks + chunk) * 8 + group % 8
     const int xcd = blockIdx.x % kXcds;
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     }
     if (single) return;
 
-    // Fold records [first, first + n) of the G heads: thread = (head mh,
+    // Fold records [first, first + n) of the G heads: thread = (head mh < GM,
     // record lane mg, float4 column md4); record lane mg takes records
     // first + mg, first + mg + MG, ... with an online max, eight records of
     // loads in flight at a time, then the record lanes meet in LDS.
@@ -595,13 +597,15 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // The loads are device-scope (sc1), which always read L2: one 128-byte
     // line holds the (max, sum) records of two sub-groups, and a copy that
     // this CU's L1 took while folding one of them could predate the other's
-    // stores.
+    // stores.  With G = 3 the threads of the padding head (mh == G) take
+    // part in the barriers only: their loads read 0 and they store nothing.
     const int mh = tid / (MG * D4), mg = (tid / D4) % MG, md4 = tid % D4;
-    static_assert(sizeof(comb_o) >= sizeof(float4) * G * MG * D4, "merge scratch");
-    static_assert(sizeof(p_lds) >= sizeof(float) * 2 * G * MG, "merge scratch");
-    float4 *mo = &comb_o[0][0][0][0];      // [G][MG][D4]
-    float *mmx = &p_lds[0][0];             // [G][MG]
-    float *mls = &p_lds[0][0] + G * MG;    // [G][MG]
+    const bool live = mh < G;
+    static_assert(sizeof(comb_o) >= sizeof(float4) * GM * MG * D4, "merge scratch");
+    static_assert(sizeof(p_lds) >= sizeof(float) * 2 * GM * MG, "merge scratch");
+    float4 *mo = &comb_o[0][0][0][0];      // [GM][MG][D4]
+    float *mmx = &p_lds[0][0];             // [GM][MG]
+    float *mls = &p_lds[0][0] + GM * MG;   // [GM][MG]
     constexpr int B = 8;  // records in flight per lane
     // Online fold of records first + c, c = c_begin, c_begin + step, ... < n,
     // into (oo, mm, ll): B records of loads in flight at a time (L2 reads).
@@ -614,8 +618,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
                 const int c = c0 + j * step;
                 const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
                 // past n: an offset at the end of the range reads 0
-                mlb[j] = buf_load2<kSc1>(wm_rsrc, c < n ? row * 8u : ws_ml_bytes);
-                ob[j] = buf_load4<kSc1>(wo_rsrc, c < n ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
+                const bool in = live && c < n;
+                mlb[j] = buf_load2<kSc1>(wm_rsrc, in ? row * 8u : ws_ml_bytes);
+                ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
             }
             float m_new = mm;
 #pragma unroll
@@ -693,13 +698,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     float Mx, Lx;
     fold(sg * kSubGroup, sg_n, ox, Mx, Lx);
     if (n_sg == 1) {
-        if (mg == 0) {
+        if (mg == 0 && live) {
             scale4(ox, 1.0f / Lx);
             out_row[md4] = ox;
         }
         return;
     }
-    if (mg == 0) {
+    if (mg == 0 && live) {
         const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(kMaxChunks + sg);
         buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, ox);
         if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(Mx, Lx));
@@ -716,7 +721,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     if (!s_last) return;
     if (tid == 0) ctr[0] = 0;
     fold(kMaxChunks, n_sg, ox, Mx, Lx);
-    if (mg == 0) {
+    if (mg == 0 && live) {
         scale4(ox, 1.0f / Lx);
         out_row[md4] = ox;
     }

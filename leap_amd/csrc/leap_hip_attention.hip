@@ -110,8 +110,8 @@ KernelFn pick_kernel(int hd, int g)
 {
 #define LEAP_CASE(HD, G) \
     if (hd == HD && g == G) return leap::decode_attention_kernel<HD, G, kWaves>;
-    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
-    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
     return nullptr;
 }

@@ -75,7 +75,7 @@ def test_reference_golden_fixtures():
 
 SHAPES = [  # n_heads, n_kv_heads, head_dim
     (32, 4, 64), (32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 2, 128), (8, 4, 64), (4, 4, 64),
-    (16, 16, 64), (8, 2, 64),
+    (16, 16, 64), (8, 2, 64), (24, 8, 128), (12, 4, 64),  # kv_mul 3: Llama-3.2-3B's 24/8 at head_dim 128
 ]
 
 

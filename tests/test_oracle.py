@@ -95,6 +95,7 @@ def test_step_reference_golden(path):
     (512, 8, 2, 3, 100, 2, 99),
     (1024, 16, 16, 1, 37, 0, 36),
     (2048, 16, 2, 2, 20, 0, 7),
+    (768, 6, 2, 2, 40, 1, 39),  # three q heads per KV head
 ])
 def test_step_live_reference(dim, nh, nkv, L, sl, layer, pos):
     if not O.ref_available():
@@ -152,7 +153,7 @@ def _bruteforce(orc, pos, q, k, v):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,T", [(4, 2, 8, 64), (4, 4, 8, 1), (8, 2, 16, 33),
-                                         (6, 3, 10, 17), (4, 1, 64, 50)])
+                                         (6, 3, 10, 17), (4, 1, 64, 50), (6, 2, 16, 29)])
 def test_step_float64_bruteforce(nh, nkv, hd, T):
     orc, pos, q, k, v = _tiny(1, nh, nkv, hd, T)
     want = _bruteforce(orc, pos, q, k, v)
