@@ -128,7 +128,7 @@ int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, in
  * l*dim*kv_dim as run_layer reads them, FloatTransformer.cpp:394-402, 664):
  * rms_att [dim], wq [dim][dim], wk [kv_dim][dim], wv [kv_dim][dim],
  * wo [dim][dim], row-major, dim = n_heads * head_dim.  The projections need
- * dim in {2048, 4096, 8192}; other sizes return -EINVAL.  Device memory for
+ * dim in {2048, 3072, 4096, 5120, 8192}; other sizes return -EINVAL.  Device memory for
  * every held layer is allocated on the first call. */
 int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const float *rms_att,
                                          const float *wq, const float *wk, const float *wv,
@@ -157,9 +157,9 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
  * (QuantizedTransformer.cpp:654-945): xb = rmsnorm(x); quantize(xb) (:338-357);
  * q, k, v = W8A8 matmul (:359-652); the fp32 attention step; quantize(out);
  * x += Wo . out.  A handle holds either fp32 or int8 weights, fixed by its
- * first set call, and one group size.  dim must be 2048, 4096 or 8192 and
- * group_size a power of two in [32, 128] (dim 2048), [32, 256] (4096) or
- * [64, 256] (8192); others return -EINVAL. */
+ * first set call, and one group size.  dim and group_size (a power of two)
+ * must be 2048 with [32, 128], 3072 with [32, 128], 4096 with [32, 256],
+ * 5120 with [64, 128] or 8192 with [64, 256]; others return -EINVAL. */
 int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, int group_size,
                                             const float *rms_att, const int8_t *wq, const float *wq_s,
                                             const int8_t *wk, const float *wk_s, const int8_t *wv,

@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "decode_attention.hpp"  // raw buffer access helpers
 #include "gemv.hpp"
 
 namespace leap {
@@ -104,6 +105,30 @@ struct Q8Row {
     int v[E / 4];
 };
 
+// The same E bytes through a raw buffer load (non-temporal): `off` past the
+// descriptor's range reads zeros without touching memory, which keeps the
+// load unconditional for lanes that own no values.
+template <int E>
+__device__ __forceinline__ Q8Row<E> load_row_buf(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    Q8Row<E> w;
+    if constexpr (E == 8) {
+        const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kNt);
+        w.v[0] = (int)a.x;
+        w.v[1] = (int)a.y;
+    } else {
+#pragma unroll
+        for (int c = 0; c < E / 16; c++) {
+            const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16u * c), 0, kNt);
+            w.v[4 * c] = (int)a.x;
+            w.v[4 * c + 1] = (int)a.y;
+            w.v[4 * c + 2] = (int)a.z;
+            w.v[4 * c + 3] = (int)a.w;
+        }
+    }
+    return w;
+}
+
 template <int E>
 __device__ __forceinline__ Q8Row<E> load_row_nt(const int8_t *p)
 {
@@ -133,11 +158,14 @@ constexpr int kQ8Waves = kQ8Threads / 64;
 
 // One workgroup of 1024 threads (16 waves, one per CU at the launch sizes
 // used) owns rows [row0, row0 + 4*RPT): four teams of 256 threads, team k
-// taking rows row0 + k*RPT + j, j < RPT.  In a team, thread t owns the E = n/256
-// values [t*E, t*E + E) of each of its rows, so a group of gs values is
-// L = gs/E adjacent lanes.  The input vector is read, normalised and quantized
-// once per workgroup, each thread taking E/4 consecutive values, and shared
-// through LDS.
+// taking rows row0 + k*RPT + j, j < RPT.  In a team, thread t < ACT owns the
+// E = n/ACT values [t*E, t*E + E) of each of its rows, so a group of gs values
+// is L = gs/E adjacent lanes.  ACT is 256 when n is 256 times a power of two;
+// for n = 3072 (ACT 192, E 16) and 5120 (ACT 160, E 32) the team's last
+// threads own no values: their row loads read zeros past the range and they
+// write nothing.  The input vector is read, normalised and quantized once per
+// workgroup, each of the first 4*ACT threads taking E/4 consecutive values,
+// and shared through LDS.
 //
 // Issue order: the input first, then the team's scales and weight rows
 // (4*RPT*n bytes per workgroup, 96 KiB for Wq/Wk/Wv at Llama-3-8B), all before
@@ -146,14 +174,17 @@ constexpr int kQ8Waves = kQ8Threads / 64;
 // runtime row count the wait for the input had to assume the longest queue,
 // which made the normalisation wait for every weight row (0.8 us at
 // Llama-3-8B).  The input work now runs while the weights stream.
-template <int E, int L, int RPT, int kIn, bool kResid>
+template <int E, int L, int RPT, int kIn, bool kResid, int ACT = kGemvThreads>
 __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
 {
-    constexpr int n = kGemvThreads * E;
-    constexpr int NG = kGemvThreads / L;   // groups per row
+    constexpr int n = ACT * E;
+    constexpr int NG = ACT / L;            // groups per row
     constexpr int VA = E / 4;              // input values per thread in the quantize step
+    constexpr int QT = n / VA;             // threads of the quantize step (4 * ACT)
     constexpr int W = (L * E) / VA;        // threads per group in the quantize step (= 4 L)
     constexpr int SLOTS = kQ8Teams * RPT;
+    static_assert(ACT <= kGemvThreads && ACT % L == 0 && ACT % 32 == 0 && NG % 4 == 0 && QT % W == 0,
+                  "thread layout");
     __shared__ __align__(16) int8_t lds_xq[n];
     __shared__ float lds_xs[NG];
     // (float)idot and ws * sx of (row slot, group), [slot][group] with the
@@ -172,7 +203,11 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
 
     // 1. the input: E/4 fp32 values (and rms weights) per thread
     float v[VA], gw[VA];
-    if constexpr (VA == 2) {
+#pragma unroll
+    for (int e = 0; e < VA; e++) v[e] = gw[e] = 0.f;
+    if (QT < kQ8Threads && tid >= QT) {
+        // owns no input values
+    } else if constexpr (VA == 2) {
         const float2 t = reinterpret_cast<const float2 *>(a.x)[tid];
         v[0] = t.x;
         v[1] = t.y;
@@ -187,7 +222,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
         }
     }
     if constexpr (kIn == kQ8InRms) {
-        if constexpr (VA == 2) {
+        if (QT < kQ8Threads && tid >= QT) {
+        } else if constexpr (VA == 2) {
             const float2 t = reinterpret_cast<const float2 *>(a.rms_w)[tid];
             gw[0] = t.x;
             gw[1] = t.y;
@@ -215,10 +251,20 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
             scv[i] = __builtin_nontemporal_load(reinterpret_cast<const gemv_f4 *>(a.ws + (size_t)r * NG + e % NG));
     }
     Q8Row<E> wv[RPT];
+    if constexpr (ACT == kGemvThreads) {
 #pragma unroll
-    for (int j = 0; j < RPT; j++) {
-        const int r = min(rbase + j, a.rows - 1);
-        wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
+        for (int j = 0; j < RPT; j++) {
+            const int r = min(rbase + j, a.rows - 1);
+            wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
+        }
+    } else {
+        const uint32_t w_bytes = (uint32_t)a.rows * (uint32_t)n;
+        const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, w_bytes);
+#pragma unroll
+        for (int j = 0; j < RPT; j++) {
+            const int r = min(rbase + j, a.rows - 1);
+            wv[j] = load_row_buf<E>(w_rsrc, tt < ACT ? (uint32_t)r * (uint32_t)n + (uint32_t)(tt * E) : w_bytes);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -247,7 +293,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
     int8_t q[VA];
 #pragma unroll
     for (int e = 0; e < VA; e++) q[e] = (int8_t)(int)roundf(v[e] * id);
-    if constexpr (VA == 2) {
+    if (QT < kQ8Threads && tid >= QT) {
+    } else if constexpr (VA == 2) {
         *reinterpret_cast<short *>(lds_xq + tid * 2) = (short)((q[0] & 0xFF) | ((q[1] & 0xFF) << 8));
     } else {
 #pragma unroll
@@ -256,7 +303,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
                 (q[4 * k] & 0xFF) | ((q[4 * k + 1] & 0xFF) << 8) | ((q[4 * k + 2] & 0xFF) << 16) |
                 ((q[4 * k + 3] & 0xFF) << 24);
     }
-    if (tid % W == 0) lds_xs[tid / W] = sx;
+    if (tid % W == 0 && tid < QT) lds_xs[tid / W] = sx;
 #pragma unroll
     for (int i = 0; i < SCL; i++) {
         const int e = 4 * (tt + i * kGemvThreads);
@@ -276,17 +323,18 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
     }
 
     // 4. exact group dot products, one (float, scale product) pair per group
+    const bool owns = ACT == kGemvThreads || tt < ACT;
     int xq[E / 4];
 #pragma unroll
-    for (int k = 0; k < E / 4; k++) xq[k] = reinterpret_cast<const int *>(lds_xq + tt * E)[k];
-    const float sxg = lds_xs[g];
+    for (int k = 0; k < E / 4; k++) xq[k] = owns ? reinterpret_cast<const int *>(lds_xq + tt * E)[k] : 0;
+    const float sxg = owns ? lds_xs[g] : 0.f;
 #pragma unroll
     for (int j = 0; j < RPT; j++) {
         int d = 0;
 #pragma unroll
         for (int k = 0; k < E / 4; k++) d = __builtin_amdgcn_sdot4(xq[k], wv[j].v[k], d, false);
         d = group_sum_i32<L>(d);
-        if (tt % L == 0) {
+        if (tt % L == 0 && owns) {
             const int at = (team * RPT + j) * NGP + g;
             lds_f[at] = (float)d;
             lds_c[at] = lds_c[at] * sxg;

@@ -241,35 +241,38 @@ bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
         *rb = proj_rows<NC>();                                                    \
         return true;                                                              \
     }
-    LEAP_PROJ(2) LEAP_PROJ(4) LEAP_PROJ(8)
+    LEAP_PROJ(2) LEAP_PROJ(3) LEAP_PROJ(4) LEAP_PROJ(5) LEAP_PROJ(8)
 #undef LEAP_PROJ
     return false;
 }
 
-// Quantized projections by n = 256 * E values per row (E per thread) and
-// group size gs = L * E.  *rpt_max is the most rows per team the kernel holds.
 using Q8Fn = void (*)(leap::Q8Args);
 
-// The int8 projection kernels by (values per thread E = dim/256, lanes per
-// group L = gs/E, rows per team RPT, input kind).  RPT is compiled in (every
-// load of a thread is then unconditional); a launch takes the smallest
-// instantiated RPT that covers its rows with one workgroup per CU.
+// The int8 projection kernels by (values per thread E, lanes per group
+// L = gs/E, rows per team RPT, input kind, threads per team that own values
+// ACT; n = ACT * E).  RPT is compiled in (every load of a thread is then
+// unconditional); a launch takes the smallest instantiated RPT that covers
+// its rows with one workgroup per CU.
 struct Q8Entry {
-    int e, l, rpt, kind;
+    int e, l, rpt, kind, act;
     Q8Fn fn;
 };
 
-#define LEAP_Q8_K(E, L, R, K) {E, L, R, K, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms>},
-#define LEAP_Q8_QKV(E, L) LEAP_Q8_K(E, L, 2, leap::kQ8InRms) LEAP_Q8_K(E, L, 3, leap::kQ8InRms) \
-    LEAP_Q8_K(E, L, 4, leap::kQ8InRms) LEAP_Q8_K(E, L, 6, leap::kQ8InRms) LEAP_Q8_K(E, L, 8, leap::kQ8InRms) \
-    LEAP_Q8_K(E, L, 10, leap::kQ8InRms)
-#define LEAP_Q8_PROJ(E, L) LEAP_Q8_K(E, L, 2, leap::kQ8InF32) LEAP_Q8_K(E, L, 4, leap::kQ8InF32) \
-    LEAP_Q8_K(E, L, 8, leap::kQ8InF32)
-#define LEAP_Q8_ALL(E, L) LEAP_Q8_QKV(E, L) LEAP_Q8_PROJ(E, L)
+#define LEAP_Q8_K(E, L, R, K, A) {E, L, R, K, A, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms, A>},
+#define LEAP_Q8_QKV(E, L, A) LEAP_Q8_K(E, L, 2, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 3, leap::kQ8InRms, A) \
+    LEAP_Q8_K(E, L, 4, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 6, leap::kQ8InRms, A)                      \
+    LEAP_Q8_K(E, L, 8, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 10, leap::kQ8InRms, A)
+#define LEAP_Q8_PROJ(E, L, A) LEAP_Q8_K(E, L, 2, leap::kQ8InF32, A) LEAP_Q8_K(E, L, 4, leap::kQ8InF32, A) \
+    LEAP_Q8_K(E, L, 8, leap::kQ8InF32, A)
+#define LEAP_Q8_ALL(E, L, A) LEAP_Q8_QKV(E, L, A) LEAP_Q8_PROJ(E, L, A)
 const Q8Entry kQ8Kernels[] = {
-    LEAP_Q8_ALL(8, 4) LEAP_Q8_ALL(8, 8) LEAP_Q8_ALL(8, 16)
-    LEAP_Q8_ALL(16, 2) LEAP_Q8_ALL(16, 4) LEAP_Q8_ALL(16, 8) LEAP_Q8_ALL(16, 16)
-    LEAP_Q8_ALL(32, 2) LEAP_Q8_ALL(32, 4) LEAP_Q8_ALL(32, 8)
+    // dim 2048, 4096, 8192: every thread of a team owns E = dim/256 values
+    LEAP_Q8_ALL(8, 4, 256) LEAP_Q8_ALL(8, 8, 256) LEAP_Q8_ALL(8, 16, 256)
+    LEAP_Q8_ALL(16, 2, 256) LEAP_Q8_ALL(16, 4, 256) LEAP_Q8_ALL(16, 8, 256) LEAP_Q8_ALL(16, 16, 256)
+    LEAP_Q8_ALL(32, 2, 256) LEAP_Q8_ALL(32, 4, 256) LEAP_Q8_ALL(32, 8, 256)
+    // dim 3072 (Llama-3.2-3B): 192 threads of 16 values; dim 5120 (Llama-2-13B): 160 of 32
+    LEAP_Q8_ALL(16, 2, 192) LEAP_Q8_ALL(16, 4, 192) LEAP_Q8_ALL(16, 8, 192)
+    LEAP_Q8_ALL(32, 2, 160) LEAP_Q8_ALL(32, 4, 160)
 };
 #undef LEAP_Q8_ALL
 #undef LEAP_Q8_PROJ
@@ -280,7 +283,7 @@ const Q8Entry kQ8Kernels[] = {
 bool q8_supported(int dim, int gs)
 {
     for (const Q8Entry &k : kQ8Kernels)
-        if (256 * k.e == dim && k.l * k.e == gs) return true;
+        if (k.act * k.e == dim && k.l * k.e == gs) return true;
     return false;
 }
 
@@ -291,7 +294,7 @@ Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
     const int need = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
     const Q8Entry *best = nullptr;
     for (const Q8Entry &k : kQ8Kernels) {
-        if (256 * k.e != dim || k.l * k.e != gs || k.kind != kind) continue;
+        if (k.act * k.e != dim || k.l * k.e != gs || k.kind != kind) continue;
         const bool covers = k.rpt >= need, best_covers = best && best->rpt >= need;
         if (!best || (covers && (!best_covers || k.rpt < best->rpt)) || (!covers && !best_covers && k.rpt > best->rpt))
             best = &k;
@@ -356,7 +359,7 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, hipStream_
     int rb;
     const int dim = h->q_dim, kv = h->kv_dim;
     if (!pick_proj(dim, &qkv, &proj, &rb))
-        return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
+        return set_err(h, -EINVAL, "dim %d: the projections need dim in {2048, 3072, 4096, 5120, 8192}", dim);
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
     leap::QkvArgs qa{};
     qa.x = x;
@@ -612,7 +615,7 @@ int leap_hip_attention_set_layer_weights(leap_hip_attention *h, int layer, const
     int rb;
     const int dim = h->q_dim, kv = h->kv_dim;
     if (!pick_proj(dim, &qkv, &proj, &rb))
-        return set_err(h, -EINVAL, "dim %d: the projections need a multiple of 1024 up to 8192", dim);
+        return set_err(h, -EINVAL, "dim %d: the projections need dim in {2048, 3072, 4096, 5120, 8192}", dim);
     if (h->w_fmt == 2) return set_err(h, -EINVAL, "this handle holds int8 weights");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     const size_t n_qkv = (size_t)(dim + 2 * kv) * dim, n_o = (size_t)dim * dim;
@@ -651,8 +654,8 @@ int leap_hip_attention_set_layer_weights_q8(leap_hip_attention *h, int layer, in
     const int dim = h->q_dim, kv = h->kv_dim, gs = group_size;
     if (!q8_supported(dim, gs))
         return set_err(h, -EINVAL,
-                       "dim %d with group size %d: the int8 projections need dim in {2048, 4096, 8192} and "
-                       "a group size of 32-128 (2048), 32-256 (4096) or 64-256 (8192)",
+                       "dim %d with group size %d: the int8 projections need dim and group size 2048 with "
+                       "32-128, 3072 with 32-128, 4096 with 32-256, 5120 with 64-128 or 8192 with 64-256",
                        dim, gs);
     if (h->w_fmt == 1) return set_err(h, -EINVAL, "this handle holds fp32 weights");
     if (h->w_fmt == 2 && gs != h->gs)

@@ -35,6 +35,8 @@ def _setup(dim, nh, nkv, seq_len, L, layers, seed):
     (8192, 64, 8, 100),   # Llama-3-70B
     (4096, 32, 32, 50),   # multi-head
     (2048, 16, 2, 1),     # first token
+    (3072, 24, 8, 200),   # Llama-3.2-3B (three q heads per KV head)
+    (5120, 40, 40, 64),   # Llama-2-13B
 ])
 def test_block_matches_oracle(hip_device, dim, nh, nkv, ctx):
     hd, L, layer = dim // nh, 2, 1

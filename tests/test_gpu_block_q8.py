@@ -115,6 +115,11 @@ def _check_stages(att, orc, layer, pos, x, got, rms, w8, gs, what):
     (8192, 64, 8, 33, 128),     # four threads per group
     (4096, 32, 8, 65, 128),     # eight threads per group at Llama-3-8B
     (2048, 16, 2, 1, 128),      # first token
+    (3072, 24, 8, 200, 64),     # Llama-3.2-3B: 192 of a team's 256 threads own values
+    (3072, 24, 8, 30, 32),
+    (3072, 24, 8, 30, 128),
+    (5120, 40, 40, 64, 64),     # Llama-2-13B: 160 threads of 32 values
+    (5120, 40, 40, 9, 128),
 ])
 def test_q8_block_stages_match_oracle(hip_device, dim, nh, nkv, ctx, gs):
     hd, L, layer = dim // nh, 2, 1

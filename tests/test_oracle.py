@@ -386,7 +386,8 @@ def test_q8_block_reference_golden(path):
     assert np.array_equal(orc.value_cache[layer, pos], fx["v_slot"])
 
 
-@pytest.mark.parametrize("n,d,gs", [(64, 4, 64), (256, 7, 32), (200, 9, 64), (4096, 40, 64), (1024, 13, 128)])
+@pytest.mark.parametrize("n,d,gs", [(64, 4, 64), (256, 7, 32), (200, 9, 64), (4096, 40, 64), (1024, 13, 128),
+                                   (3072, 11, 64), (5120, 5, 128)])
 def test_q8_quantize_matmul_live_reference(n, d, gs):
     if not O.ref_q8_available():
         pytest.skip("quantized reference driver not built (reference sources absent)")
