@@ -15,7 +15,11 @@ the 8 TB/s HBM peak alongside.
 
 The CPU baseline is the oracle (the restated reference attention, OpenMP over
 heads, AVX2) timed on the host cores on a bounded sample of the same workload:
-the same device bytes of a few layers of sequence 0, downloaded.
+the same device bytes of a few layers of sequence 0, downloaded.  The
+reference keeps its attention inline in run_layer, between the projections,
+so it cannot be timed on the attention alone.  For the sub-block workloads it
+can: there the baseline is the reference's own run_layer (oracle/_ref, built
+from its sources) when that library is present.
 
 The `*-block-*` workloads time the whole attention sub-block of the layer step
 instead (rmsnorm, q/k/v projections, attention, wo projection and residual;
@@ -134,24 +138,52 @@ def contexts(workload: str):
 
 
 def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights, q8: bool = False):
-    """The oracle's sub-block chain (rmsnorm, matmul, attention, matmul,
-    residual), OpenMP over rows and heads, on the host, on layers
-    [0, n_layers_sample) with the device cache bytes downloaded."""
+    """The sub-block on the host cores, on the device cache bytes of layer 0
+    (downloaded): the reference's own run_layer (oracle/_ref, compiled from
+    its sources with its release flags, OpenMP as it ships) on a one-layer
+    engine with these weights and a zero FFN of negligible size, when that
+    library is present; otherwise the oracle's chain (rmsnorm, matmul,
+    attention, matmul, residual) on layers [0, n_layers_sample)."""
     from oracle import oracle as O
     L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    T = int(Ts[0])
+    x0 = np.random.default_rng(SEED + sidx).standard_normal(nh * hd).astype(np.float32)
+    nbytes = (q8_block_bytes if q8 else block_bytes)(T, nh, nkv, hd)
+    if (O.ref_q8_available() if q8 else O.ref_available()) and theta == 500000.0:
+        k, v = att.kv_download(0, 0, 0, T - 1)
+        timer = O.RefBlockTimer(nh * hd, nh, nkv, T, *weights, k, v, gs=Q8_GROUP if q8 else None)
+        try:
+            x = x0.copy()
+            timer.run(T - 1, x, 1)  # the OpenMP pool starts
+            times = []
+            t_end = time.perf_counter() + budget_s
+            while time.perf_counter() < t_end or len(times) < 3:
+                x[:] = x0
+                times.append(timer.run(T - 1, x, 1))
+        finally:
+            timer.close()
+        us = float(np.median(times)) * 1e6
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+        return {
+            "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+            "us_per_layer_step": round(us, 2),
+            "sample": f"{len(times)} calls of the reference's {'QuantizedTransformer' if q8 else 'FloatTransformer'}"
+                      f"::run_layer at pos {T - 1} on a one-layer engine holding the workload's weights "
+                      f"(zero FFN of hidden size {Q8_GROUP if q8 else 8}) and layer 0's device cache rows; "
+                      f"median per call; the reference's own OpenMP",
+        }
     if not os.path.isfile(O.ORACLE_SO):
         O.build(ref=False)
     env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
     threads = min(env_threads or os.cpu_count() or 1, 16)
     O.lib().oracle_set_threads(threads)
-    T = int(Ts[0])
     n_l = min(n_layers_sample, L)
     orc = O.Oracle(n_l, nh, nkv, hd, T, theta=theta)
     for l in range(n_l):
         k, v = att.kv_download(0, l, 0, T)
         orc.key_cache[l] = k
         orc.value_cache[l] = v
-    x = np.random.default_rng(SEED + sidx).standard_normal(nh * hd).astype(np.float32)
+    x = x0
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or len(times) < 3:
@@ -163,9 +195,8 @@ def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float,
                 orc.block(l, T - 1, x, *weights)
         times.append((time.perf_counter() - t0) / n_l)
     us = float(np.median(times)) * 1e6
-    gbs = (q8_block_bytes if q8 else block_bytes)(T, nh, nkv, hd) / (us * 1e-6) / 1e9
     return {
-        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "us_per_layer_step": round(us, 2),
         "sample": f"{len(times)} sweeps of the sub-block over layers 0..{n_l - 1} of the same workload "
                   f"(context {T}), device cache bytes downloaded; median per layer-step; OpenMP over "

@@ -108,6 +108,12 @@ def ref():
         L.leapref_matmul.restype = _I
         L.leapref_block.argtypes = [_I] * 7 + [_F] * 8
         L.leapref_block.restype = _I
+        L.leapref_block_timer_create.argtypes = [_I] * 4 + [_F] * 7 + [_I]
+        L.leapref_block_timer_create.restype = ctypes.c_void_p
+        L.leapref_block_timer_run.argtypes = [ctypes.c_void_p, _I, _F, _I]
+        L.leapref_block_timer_run.restype = ctypes.c_double
+        L.leapref_block_timer_destroy.argtypes = [ctypes.c_void_p]
+        L.leapref_block_timer_destroy.restype = None
         _ref = L
     return _ref
 
@@ -128,6 +134,12 @@ def ref_q8():
         L.leapref_q8_matmul.restype = _I
         L.leapref_q8_block.argtypes = [_I] * 8 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _F]
         L.leapref_q8_block.restype = _I
+        L.leapref_q8_block_timer_create.argtypes = [_I] * 5 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _I]
+        L.leapref_q8_block_timer_create.restype = ctypes.c_void_p
+        L.leapref_q8_block_timer_run.argtypes = [ctypes.c_void_p, _I, _F, _I]
+        L.leapref_q8_block_timer_run.restype = ctypes.c_double
+        L.leapref_q8_block_timer_destroy.argtypes = [ctypes.c_void_p]
+        L.leapref_q8_block_timer_destroy.restype = None
         _ref_q8 = L
     return _ref_q8
 
@@ -446,6 +458,49 @@ def ref_q8_block(dim, n_heads, n_kv_heads, n_layers, seq_len, gs, layer, pos, x,
     if rc != 0:
         raise RuntimeError("reference q8 block failed")
     return xo, kc, vc
+
+
+class RefBlockTimer:
+    """The reference's own run_layer (oracle/_ref) on a one-layer engine that
+    holds the given attention weights (fp32 arrays, or (int8, scales) pairs
+    with group size gs), a zero FFN of negligible size, and cache rows
+    [0, rows) from key_rows/value_rows: the CPU baseline of the sub-block."""
+
+    def __init__(self, dim, n_heads, n_kv_heads, seq_len, rms_att, wq, wk, wv, wo, key_rows, value_rows,
+                 gs=None):
+        self._keep = [_c32(rms_att), _c32(key_rows), _c32(value_rows)]
+        rows = key_rows.shape[0]
+        if gs is None:
+            self.lib = ref()
+            ws = [_c32(w) for w in (wq, wk, wv, wo)]
+            self._keep += ws
+            self.h = self.lib.leapref_block_timer_create(dim, n_heads, n_kv_heads, seq_len, _fp(self._keep[0]),
+                                                         *[_fp(w) for w in ws], _fp(self._keep[1]),
+                                                         _fp(self._keep[2]), rows)
+            self._run, self._free = self.lib.leapref_block_timer_run, self.lib.leapref_block_timer_destroy
+        else:
+            self.lib = ref_q8()
+            args = []
+            for w in (wq, wk, wv, wo):
+                q, sc = np.ascontiguousarray(w[0], np.int8), _c32(w[1])
+                self._keep += [q, sc]
+                args += [_bp(q), _fp(sc)]
+            self.h = self.lib.leapref_q8_block_timer_create(dim, n_heads, n_kv_heads, seq_len, gs,
+                                                            _fp(self._keep[0]), *args, _fp(self._keep[1]),
+                                                            _fp(self._keep[2]), rows)
+            self._run, self._free = self.lib.leapref_q8_block_timer_run, self.lib.leapref_q8_block_timer_destroy
+        if not self.h:
+            raise RuntimeError("reference block timer failed")
+
+    def run(self, pos, x, iters):
+        """Seconds per run_layer(0, pos, x) over `iters` calls (x is updated)."""
+        assert x.dtype == np.float32 and x.flags.c_contiguous
+        return self._run(self.h, pos, _fp(x), iters)
+
+    def close(self):
+        if self.h:
+            self._free(self.h)
+            self.h = None
 
 
 def ref_rope_table(dim, n_heads, seq_len):

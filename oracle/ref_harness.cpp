@@ -27,6 +27,8 @@
 
 // run_layer, rmsnorm, matmul and the run state are private members of the
 // reference class; this test driver opens them up for itself only.
+#include <chrono>
+
 #define private public
 #include "FloatTransformer.h"
 #undef private
@@ -71,6 +73,11 @@ std::unique_ptr<FloatTransformer> make_engine(const Config &c, const float *wq, 
     if (rms_att) std::memcpy(p + (size_t)layer * dim, rms_att, sizeof(float) * dim);
     return std::make_unique<FloatTransformer>(c, -1, MAP_FAILED, 0, w.buf.data(), 1);
 }
+
+struct BlockTimer {
+    Weights w;
+    std::unique_ptr<FloatTransformer> eng;
+};
 
 Config make_config(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len)
 {
@@ -187,6 +194,40 @@ int leapref_block(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_le
         return -1;
     }
 }
+
+// For timing the reference's sub-block on the host: an engine of one layer
+// (index 0) with the given rms_att, wq, wk, wv, wo, a zero FFN of hidden size
+// 8 (its cost is negligible next to the attention weights), and cache rows
+// [0, rows) set from key_rows/value_rows ([rows][kv_dim]).  NULL on failure.
+void *leapref_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, const float *rms_att,
+                                 const float *wq, const float *wk, const float *wv, const float *wo,
+                                 const float *key_rows, const float *value_rows, int rows)
+{
+    try {
+        Config c = make_config(dim, n_heads, n_kv_heads, 1, seq_len);
+        auto t = std::make_unique<BlockTimer>();
+        t->eng = make_engine(c, wq, wk, wv, 0, t->w, rms_att, wo);
+        const size_t n = (size_t)rows * n_kv_heads * (dim / n_heads);
+        std::memcpy(t->eng->state.key_cache.data(), key_rows, sizeof(float) * n);
+        std::memcpy(t->eng->state.value_cache.data(), value_rows, sizeof(float) * n);
+        return t.release();
+    } catch (const std::exception &e) {
+        std::cerr << "leapref_block_timer_create: " << e.what() << "\n";
+        return nullptr;
+    }
+}
+
+// run_layer(0, pos, x) `iters` times on the timer's engine (x updated in
+// place each time); returns the mean seconds per call.
+double leapref_block_timer_run(void *timer, int pos, float *x, int iters)
+{
+    auto *t = static_cast<BlockTimer *>(timer);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < iters; i++) t->eng->run_layer(0, pos, x);
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() / iters;
+}
+
+void leapref_block_timer_destroy(void *timer) { delete static_cast<BlockTimer *>(timer); }
 
 // clear_kv_cache (FloatTransformer.cpp:74-77) on a filled engine; returns the
 // number of nonzero floats left in either cache (0 expected).

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <iostream>
 #include <memory>
+#include <chrono>
 #include <stdexcept>
 #include <vector>
 #include <sys/mman.h>
@@ -108,6 +109,11 @@ std::unique_ptr<QuantizedTransformer> make_engine(const Config &c, int gs, Blob 
     return std::make_unique<QuantizedTransformer>(c, -1, MAP_FAILED, 0, b.buf.data(), 1, gs);
 }
 
+struct BlockTimer {
+    Blob b;
+    std::unique_ptr<QuantizedTransformer> eng;
+};
+
 }  // namespace
 
 extern "C" {
@@ -174,5 +180,40 @@ int leapref_q8_block(int dim, int n_heads, int n_kv_heads, int n_layers, int seq
         return -1;
     }
 }
+
+// For timing the reference's int8 sub-block on the host: an engine of one
+// layer (index 0) with the given weights, a zero FFN of hidden size gs, and
+// cache rows [0, rows) set from key_rows/value_rows ([rows][kv_dim]).  NULL
+// on failure.
+void *leapref_q8_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, int gs, const float *rms_att,
+                                    const int8_t *wq_q, const float *wq_s, const int8_t *wk_q, const float *wk_s,
+                                    const int8_t *wv_q, const float *wv_s, const int8_t *wo_q, const float *wo_s,
+                                    const float *key_rows, const float *value_rows, int rows)
+{
+    try {
+        const Config c = make_config(dim, n_heads, n_kv_heads, 1, seq_len, gs);
+        const LayerQ8 lw{rms_att, wq_q, wk_q, wv_q, wo_q, wq_s, wk_s, wv_s, wo_s};
+        auto t = std::make_unique<BlockTimer>();
+        t->eng = make_engine(c, gs, t->b, 0, &lw);
+        const size_t n = (size_t)rows * n_kv_heads * (dim / n_heads);
+        std::memcpy(t->eng->state.key_cache.data(), key_rows, sizeof(float) * n);
+        std::memcpy(t->eng->state.value_cache.data(), value_rows, sizeof(float) * n);
+        return t.release();
+    } catch (const std::exception &e) {
+        std::cerr << "leapref_q8_block_timer_create: " << e.what() << "\n";
+        return nullptr;
+    }
+}
+
+// run_layer(0, pos, x) `iters` times; the mean seconds per call.
+double leapref_q8_block_timer_run(void *timer, int pos, float *x, int iters)
+{
+    auto *t = static_cast<BlockTimer *>(timer);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < iters; i++) t->eng->run_layer(0, pos, x);
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() / iters;
+}
+
+void leapref_q8_block_timer_destroy(void *timer) { delete static_cast<BlockTimer *>(timer); }
 
 }  // extern "C"
