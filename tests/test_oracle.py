@@ -491,3 +491,28 @@ def test_rejects_bad_arguments():
     orc = O.Oracle(1, 4, 2, 8, 16)
     with pytest.raises(ValueError):
         orc.step(0, 16, np.zeros(32, np.float32), np.zeros(16, np.float32), np.zeros(16, np.float32))
+
+
+@pytest.mark.parametrize("gs", [None, 64])
+def test_reference_block_timer_runs_the_reference(gs):
+    """The CPU-baseline timer (the reference's run_layer on a one-layer
+    engine) computes what the oracle's chain computes, bit for bit."""
+    if not (O.ref_q8_available() if gs else O.ref_available()):
+        pytest.skip("reference driver not built (reference sources absent)")
+    dim, nh, nkv, T = 512, 8, 2, 70
+    hd, kv = dim // nh, nkv * (dim // nh)
+    x0, rms, *wf = block_inputs(rng_for(dim, T, 81), dim, kv)
+    w = [O.quantize_weight(m, gs) for m in wf] if gs else wf
+    rng = rng_for(dim, T, 82)
+    k, v = normal(rng, (T, kv), hd), normal(rng, (T, kv), hd)
+    timer = O.RefBlockTimer(dim, nh, nkv, T + 1, rms, *w, k, v, gs=gs)
+    try:
+        x = x0.copy()
+        assert timer.run(T, x, 1) > 0
+    finally:
+        timer.close()
+    orc = O.Oracle(1, nh, nkv, hd, T + 1)
+    orc.key_cache[0, :T] = k
+    orc.value_cache[0, :T] = v
+    want = orc.block_q8(0, T, x0, rms, *w, gs) if gs else orc.block(0, T, x0, rms, *w)
+    assert np.array_equal(x, want)
