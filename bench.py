@@ -139,11 +139,12 @@ def contexts(workload: str):
 
 def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights, q8: bool = False):
     """The sub-block on the host cores, on the device cache bytes of layer 0
-    (downloaded): the reference's own run_layer (oracle/_ref, compiled from
-    its sources with its release flags, OpenMP as it ships) on a one-layer
-    engine with these weights and a zero FFN of negligible size, when that
-    library is present; otherwise the oracle's chain (rmsnorm, matmul,
-    attention, matmul, residual) on layers [0, n_layers_sample)."""
+    (downloaded).  When oracle/_ref is present: the reference's own run_layer
+    (compiled from its sources with its release flags, OpenMP as it ships) on
+    an engine whose layers each hold these weights and a zero FFN of
+    negligible size, cycled so that the weights come from memory.  Otherwise:
+    the oracle's chain (rmsnorm, matmul, attention, matmul, residual) on layers
+    [0, n_layers_sample)."""
     from oracle import oracle as O
     L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
     T = int(Ts[0])
@@ -151,7 +152,10 @@ def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float,
     nbytes = (q8_block_bytes if q8 else block_bytes)(T, nh, nkv, hd)
     if (O.ref_q8_available() if q8 else O.ref_available()) and theta == 500000.0:
         k, v = att.kv_download(0, 0, 0, T - 1)
-        timer = O.RefBlockTimer(nh * hd, nh, nkv, T, *weights, k, v, gs=Q8_GROUP if q8 else None)
+        # enough layers (each its own copy of the weights and cache rows) that
+        # the CPU caches cannot hold them: about 1.6 GB
+        n_l = max(4, -(-1_600_000_000 // nbytes))
+        timer = O.RefBlockTimer(nh * hd, nh, nkv, T, *weights, k, v, gs=Q8_GROUP if q8 else None, n_layers=n_l)
         try:
             x = x0.copy()
             timer.run(T - 1, x, 1)  # the OpenMP pool starts
@@ -168,9 +172,9 @@ def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float,
             "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
             "us_per_layer_step": round(us, 2),
             "sample": f"{len(times)} calls of the reference's {'QuantizedTransformer' if q8 else 'FloatTransformer'}"
-                      f"::run_layer at pos {T - 1} on a one-layer engine holding the workload's weights "
-                      f"(zero FFN of hidden size {Q8_GROUP if q8 else 8}) and layer 0's device cache rows; "
-                      f"median per call; the reference's own OpenMP",
+                      f"::run_layer at pos {T - 1}, cycling through an engine of {n_l} layers that each hold "
+                      f"the workload's weights (zero FFN of hidden size {Q8_GROUP if q8 else 8}) and layer 0's "
+                      f"device cache rows; median per call; the reference's own OpenMP",
         }
     if not os.path.isfile(O.ORACLE_SO):
         O.build(ref=False)

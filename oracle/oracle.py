@@ -108,7 +108,7 @@ def ref():
         L.leapref_matmul.restype = _I
         L.leapref_block.argtypes = [_I] * 7 + [_F] * 8
         L.leapref_block.restype = _I
-        L.leapref_block_timer_create.argtypes = [_I] * 4 + [_F] * 7 + [_I]
+        L.leapref_block_timer_create.argtypes = [_I] * 5 + [_F] * 7 + [_I]
         L.leapref_block_timer_create.restype = ctypes.c_void_p
         L.leapref_block_timer_run.argtypes = [ctypes.c_void_p, _I, _F, _I]
         L.leapref_block_timer_run.restype = ctypes.c_double
@@ -134,7 +134,7 @@ def ref_q8():
         L.leapref_q8_matmul.restype = _I
         L.leapref_q8_block.argtypes = [_I] * 8 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _F]
         L.leapref_q8_block.restype = _I
-        L.leapref_q8_block_timer_create.argtypes = [_I] * 5 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _I]
+        L.leapref_q8_block_timer_create.argtypes = [_I] * 6 + [_F, _B, _F, _B, _F, _B, _F, _B, _F, _F, _F, _I]
         L.leapref_q8_block_timer_create.restype = ctypes.c_void_p
         L.leapref_q8_block_timer_run.argtypes = [ctypes.c_void_p, _I, _F, _I]
         L.leapref_q8_block_timer_run.restype = ctypes.c_double
@@ -461,20 +461,22 @@ def ref_q8_block(dim, n_heads, n_kv_heads, n_layers, seq_len, gs, layer, pos, x,
 
 
 class RefBlockTimer:
-    """The reference's own run_layer (oracle/_ref) on a one-layer engine that
-    holds the given attention weights (fp32 arrays, or (int8, scales) pairs
-    with group size gs), a zero FFN of negligible size, and cache rows
-    [0, rows) from key_rows/value_rows: the CPU baseline of the sub-block."""
+    """The reference's own run_layer (oracle/_ref) on an engine of n_layers
+    layers that each hold the given attention weights (fp32 arrays, or (int8,
+    scales) pairs with group size gs), a zero FFN of negligible size, and
+    cache rows [0, rows) from key_rows/value_rows; each call runs the next
+    layer.  The CPU baseline of the sub-block."""
 
     def __init__(self, dim, n_heads, n_kv_heads, seq_len, rms_att, wq, wk, wv, wo, key_rows, value_rows,
-                 gs=None):
+                 gs=None, n_layers=1):
         self._keep = [_c32(rms_att), _c32(key_rows), _c32(value_rows)]
         rows = key_rows.shape[0]
         if gs is None:
             self.lib = ref()
             ws = [_c32(w) for w in (wq, wk, wv, wo)]
             self._keep += ws
-            self.h = self.lib.leapref_block_timer_create(dim, n_heads, n_kv_heads, seq_len, _fp(self._keep[0]),
+            self.h = self.lib.leapref_block_timer_create(dim, n_heads, n_kv_heads, seq_len, n_layers,
+                                                         _fp(self._keep[0]),
                                                          *[_fp(w) for w in ws], _fp(self._keep[1]),
                                                          _fp(self._keep[2]), rows)
             self._run, self._free = self.lib.leapref_block_timer_run, self.lib.leapref_block_timer_destroy
@@ -485,7 +487,7 @@ class RefBlockTimer:
                 q, sc = np.ascontiguousarray(w[0], np.int8), _c32(w[1])
                 self._keep += [q, sc]
                 args += [_bp(q), _fp(sc)]
-            self.h = self.lib.leapref_q8_block_timer_create(dim, n_heads, n_kv_heads, seq_len, gs,
+            self.h = self.lib.leapref_q8_block_timer_create(dim, n_heads, n_kv_heads, seq_len, n_layers, gs,
                                                             _fp(self._keep[0]), *args, _fp(self._keep[1]),
                                                             _fp(self._keep[2]), rows)
             self._run, self._free = self.lib.leapref_q8_block_timer_run, self.lib.leapref_q8_block_timer_destroy
@@ -493,7 +495,7 @@ class RefBlockTimer:
             raise RuntimeError("reference block timer failed")
 
     def run(self, pos, x, iters):
-        """Seconds per run_layer(0, pos, x) over `iters` calls (x is updated)."""
+        """Seconds per run_layer(l, pos, x) over `iters` calls, l cycling (x is updated)."""
         assert x.dtype == np.float32 and x.flags.c_contiguous
         return self._run(self.h, pos, _fp(x), iters)
 

@@ -77,6 +77,7 @@ std::unique_ptr<FloatTransformer> make_engine(const Config &c, const float *wq, 
 struct BlockTimer {
     Weights w;
     std::unique_ptr<FloatTransformer> eng;
+    int n_layers = 1, next = 0;
 };
 
 Config make_config(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_len)
@@ -195,21 +196,36 @@ int leapref_block(int dim, int n_heads, int n_kv_heads, int n_layers, int seq_le
     }
 }
 
-// For timing the reference's sub-block on the host: an engine of one layer
-// (index 0) with the given rms_att, wq, wk, wv, wo, a zero FFN of hidden size
-// 8 (its cost is negligible next to the attention weights), and cache rows
-// [0, rows) set from key_rows/value_rows ([rows][kv_dim]).  NULL on failure.
-void *leapref_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, const float *rms_att,
-                                 const float *wq, const float *wk, const float *wv, const float *wo,
-                                 const float *key_rows, const float *value_rows, int rows)
+// For timing the reference's sub-block on the host: an engine of n_layers
+// layers, each holding the given rms_att, wq, wk, wv, wo (copies at their own
+// addresses, so that cycling through the layers streams the weights from
+// memory as a real engine does rather than from the CPU caches), a zero FFN
+// of hidden size 8 (negligible next to the attention weights), and cache
+// rows [0, rows) set from key_rows/value_rows ([rows][kv_dim]).  NULL on
+// failure.
+void *leapref_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, int n_layers,
+                                 const float *rms_att, const float *wq, const float *wk, const float *wv,
+                                 const float *wo, const float *key_rows, const float *value_rows, int rows)
 {
     try {
-        Config c = make_config(dim, n_heads, n_kv_heads, 1, seq_len);
+        Config c = make_config(dim, n_heads, n_kv_heads, n_layers, seq_len);
         auto t = std::make_unique<BlockTimer>();
         t->eng = make_engine(c, wq, wk, wv, 0, t->w, rms_att, wo);
-        const size_t n = (size_t)rows * n_kv_heads * (dim / n_heads);
-        std::memcpy(t->eng->state.key_cache.data(), key_rows, sizeof(float) * n);
-        std::memcpy(t->eng->state.value_cache.data(), value_rows, sizeof(float) * n);
+        const size_t d = dim, kv = (size_t)n_kv_heads * (dim / n_heads);
+        auto &W = t->eng->weights;
+        for (int l = 1; l < n_layers; l++) {  // the blob is ours: copy layer 0's slices
+            std::memcpy(const_cast<float *>(W.rms_att_weight) + l * d, W.rms_att_weight, sizeof(float) * d);
+            std::memcpy(const_cast<float *>(W.wq) + l * d * d, W.wq, sizeof(float) * d * d);
+            std::memcpy(const_cast<float *>(W.wk) + l * d * kv, W.wk, sizeof(float) * d * kv);
+            std::memcpy(const_cast<float *>(W.wv) + l * d * kv, W.wv, sizeof(float) * d * kv);
+            std::memcpy(const_cast<float *>(W.wo) + l * d * d, W.wo, sizeof(float) * d * d);
+        }
+        for (int l = 0; l < n_layers; l++) {
+            const size_t off = (size_t)l * seq_len * kv;
+            std::memcpy(t->eng->state.key_cache.data() + off, key_rows, sizeof(float) * rows * kv);
+            std::memcpy(t->eng->state.value_cache.data() + off, value_rows, sizeof(float) * rows * kv);
+        }
+        t->n_layers = n_layers;
         return t.release();
     } catch (const std::exception &e) {
         std::cerr << "leapref_block_timer_create: " << e.what() << "\n";
@@ -217,13 +233,16 @@ void *leapref_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_l
     }
 }
 
-// run_layer(0, pos, x) `iters` times on the timer's engine (x updated in
-// place each time); returns the mean seconds per call.
+// run_layer(l, pos, x) `iters` times, l cycling through the layers (x
+// updated in place each time); returns the mean seconds per call.
 double leapref_block_timer_run(void *timer, int pos, float *x, int iters)
 {
     auto *t = static_cast<BlockTimer *>(timer);
     const auto t0 = std::chrono::steady_clock::now();
-    for (int i = 0; i < iters; i++) t->eng->run_layer(0, pos, x);
+    for (int i = 0; i < iters; i++) {
+        t->eng->run_layer(t->next, pos, x);
+        t->next = (t->next + 1) % t->n_layers;
+    }
     return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() / iters;
 }
 

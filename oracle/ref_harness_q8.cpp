@@ -112,6 +112,7 @@ std::unique_ptr<QuantizedTransformer> make_engine(const Config &c, int gs, Blob 
 struct BlockTimer {
     Blob b;
     std::unique_ptr<QuantizedTransformer> eng;
+    int n_layers = 1, next = 0;
 };
 
 }  // namespace
@@ -181,23 +182,38 @@ int leapref_q8_block(int dim, int n_heads, int n_kv_heads, int n_layers, int seq
     }
 }
 
-// For timing the reference's int8 sub-block on the host: an engine of one
-// layer (index 0) with the given weights, a zero FFN of hidden size gs, and
-// cache rows [0, rows) set from key_rows/value_rows ([rows][kv_dim]).  NULL
-// on failure.
-void *leapref_q8_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, int gs, const float *rms_att,
-                                    const int8_t *wq_q, const float *wq_s, const int8_t *wk_q, const float *wk_s,
-                                    const int8_t *wv_q, const float *wv_s, const int8_t *wo_q, const float *wo_s,
-                                    const float *key_rows, const float *value_rows, int rows)
+// For timing the reference's int8 sub-block on the host: an engine of
+// n_layers layers, each holding copies of the given weights at its own
+// addresses (cycling through them streams the weights from memory, as a real
+// engine does), a zero FFN of hidden size gs, and cache rows [0, rows) set
+// from key_rows/value_rows ([rows][kv_dim]).  NULL on failure.
+void *leapref_q8_block_timer_create(int dim, int n_heads, int n_kv_heads, int seq_len, int n_layers, int gs,
+                                    const float *rms_att, const int8_t *wq_q, const float *wq_s, const int8_t *wk_q,
+                                    const float *wk_s, const int8_t *wv_q, const float *wv_s, const int8_t *wo_q,
+                                    const float *wo_s, const float *key_rows, const float *value_rows, int rows)
 {
     try {
-        const Config c = make_config(dim, n_heads, n_kv_heads, 1, seq_len, gs);
+        const Config c = make_config(dim, n_heads, n_kv_heads, n_layers, seq_len, gs);
         const LayerQ8 lw{rms_att, wq_q, wk_q, wv_q, wo_q, wq_s, wk_s, wv_s, wo_s};
         auto t = std::make_unique<BlockTimer>();
         t->eng = make_engine(c, gs, t->b, 0, &lw);
-        const size_t n = (size_t)rows * n_kv_heads * (dim / n_heads);
-        std::memcpy(t->eng->state.key_cache.data(), key_rows, sizeof(float) * n);
-        std::memcpy(t->eng->state.value_cache.data(), value_rows, sizeof(float) * n);
+        const size_t d = dim, kv = (size_t)n_kv_heads * (dim / n_heads);
+        auto &W = t->eng->weights;
+        const size_t per[4] = {d * d, kv * d, kv * d, d * d};
+        std::vector<QuantizedTensor> *ts[4] = {&W.wq, &W.wk, &W.wv, &W.wo};
+        for (int l = 1; l < n_layers; l++) {  // the blob is ours: copy layer 0's tensors
+            std::memcpy(W.rms_att_weight + l * d, W.rms_att_weight, sizeof(float) * d);
+            for (int k = 0; k < 4; k++) {
+                std::memcpy((*ts[k])[l].q, (*ts[k])[0].q, per[k]);
+                std::memcpy((*ts[k])[l].s, (*ts[k])[0].s, sizeof(float) * (per[k] / gs));
+            }
+        }
+        for (int l = 0; l < n_layers; l++) {
+            const size_t off = (size_t)l * seq_len * kv;
+            std::memcpy(t->eng->state.key_cache.data() + off, key_rows, sizeof(float) * rows * kv);
+            std::memcpy(t->eng->state.value_cache.data() + off, value_rows, sizeof(float) * rows * kv);
+        }
+        t->n_layers = n_layers;
         return t.release();
     } catch (const std::exception &e) {
         std::cerr << "leapref_q8_block_timer_create: " << e.what() << "\n";
@@ -205,12 +221,16 @@ void *leapref_q8_block_timer_create(int dim, int n_heads, int n_kv_heads, int se
     }
 }
 
-// run_layer(0, pos, x) `iters` times; the mean seconds per call.
+// run_layer(l, pos, x) `iters` times, l cycling through the layers; the mean
+// seconds per call.
 double leapref_q8_block_timer_run(void *timer, int pos, float *x, int iters)
 {
     auto *t = static_cast<BlockTimer *>(timer);
     const auto t0 = std::chrono::steady_clock::now();
-    for (int i = 0; i < iters; i++) t->eng->run_layer(0, pos, x);
+    for (int i = 0; i < iters; i++) {
+        t->eng->run_layer(t->next, pos, x);
+        t->next = (t->next + 1) % t->n_layers;
+    }
     return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() / iters;
 }
 

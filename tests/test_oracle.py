@@ -505,14 +505,15 @@ def test_reference_block_timer_runs_the_reference(gs):
     w = [O.quantize_weight(m, gs) for m in wf] if gs else wf
     rng = rng_for(dim, T, 82)
     k, v = normal(rng, (T, kv), hd), normal(rng, (T, kv), hd)
-    timer = O.RefBlockTimer(dim, nh, nkv, T + 1, rms, *w, k, v, gs=gs)
-    try:
-        x = x0.copy()
-        assert timer.run(T, x, 1) > 0
-    finally:
-        timer.close()
     orc = O.Oracle(1, nh, nkv, hd, T + 1)
     orc.key_cache[0, :T] = k
     orc.value_cache[0, :T] = v
     want = orc.block_q8(0, T, x0, rms, *w, gs) if gs else orc.block(0, T, x0, rms, *w)
-    assert np.array_equal(x, want)
+    timer = O.RefBlockTimer(dim, nh, nkv, T + 1, rms, *w, k, v, gs=gs, n_layers=3)
+    try:
+        for layer in range(3):  # each call runs the next layer, all holding the same weights and rows
+            x = x0.copy()
+            assert timer.run(T, x, 1) > 0
+            assert np.array_equal(x, want), f"layer {layer}"
+    finally:
+        timer.close()
