@@ -13,13 +13,15 @@ timed region, with B(T) = 8*T*kv_dim + 8*dim + 16*kv_dim + 4*head_dim bytes
 per layer-step and sequence; microseconds per layer-step and the fraction of
 the 8 TB/s HBM peak alongside.
 
-The CPU baseline is the oracle (the restated reference attention, OpenMP over
-heads, AVX2) timed on the host cores on a bounded sample of the same workload:
-the same device bytes of a few layers of sequence 0, downloaded.  The
-reference keeps its attention inline in run_layer, between the projections,
-so it cannot be timed on the attention alone.  For the sub-block workloads it
-can: there the baseline is the reference's own run_layer (oracle/_ref, built
-from its sources) when that library is present.
+The CPU baseline is the reference's own code (oracle/_ref, built from its
+sources with its release flags) timed on the host cores on a bounded sample of
+the same workload, with sequence 0's device cache bytes downloaded.  The
+reference keeps its attention inline in run_layer, between the projections:
+for the attention workloads, calls at the workload's position and at position
+0 alternate, and the difference of their medians is the attention; for the
+sub-block workloads, run_layer itself is timed (zero FFN).  Without that
+library (or for a RoPE base other than the reference's fixed 500000), the
+oracle, the restated reference (OpenMP over heads, AVX2), is timed instead.
 
 The `*-block-*` workloads time the whole attention sub-block of the layer step
 instead (rmsnorm, q/k/v projections, attention, wo projection and residual;
@@ -208,12 +210,61 @@ def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float,
     }
 
 
-def cpu_baseline(att, workload, Ts, n_layers_sample: int, budget_s: float):
-    """Time the oracle on the host on layers [0, n_layers_sample) of sequence
-    0 of the device cache (downloaded bytes), repeating sweeps for about
-    budget_s seconds."""
+def cpu_baseline_reference(att, workload, T: int, budget_s: float):
+    """The reference's own attention on the host cores, timed through its
+    run_layer (oracle/_ref), which holds the attention inline between the
+    projections: calls at pos T-1 and at pos 0 alternate on an engine of
+    several layers (each its own copy of synthetic weights and of sequence
+    0's first T-1 device cache rows, cycled so that nothing stays in the CPU
+    caches), and the difference of their medians is the attention over T
+    rows; the projections, the residual and the zero FFN are the same work
+    in both."""
     from oracle import oracle as O
     L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    dim, kvd = nh * hd, nkv * hd
+    wrng = np.random.default_rng(SEED + sidx)
+    w = [(1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32)] + [
+        (wrng.standard_normal(shape) / np.sqrt(dim)).astype(np.float32)
+        for shape in ((dim, dim), (kvd, dim), (kvd, dim), (dim, dim))]
+    k, v = att.kv_download(0, 0, 0, T - 1)
+    per_layer = 4 * (2 * dim * dim + 2 * kvd * dim) + 8 * T * kvd
+    n_l = max(4, -(-1_600_000_000 // per_layer))
+    timer = O.RefBlockTimer(dim, nh, nkv, T, *w, k, v, n_layers=n_l)
+    x0 = wrng.standard_normal(dim).astype(np.float32)
+    x = x0.copy()
+    long_t, short_t = [], []
+    try:
+        timer.run(T - 1, x, n_l)  # the OpenMP pool starts, every layer touched once
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(long_t) < 5:
+            x[:] = x0
+            long_t.append(timer.run(T - 1, x, 1))
+            x[:] = x0
+            short_t.append(timer.run(0, x, 1))
+    finally:
+        timer.close()
+    us = (float(np.median(long_t)) - float(np.median(short_t))) * 1e6
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+    return {
+        "value": round(algorithmic_bytes(T, nh, nkv, hd) / (us * 1e-6) / 1e9, 3), "unit": "GB/s",
+        "cores": threads, "kind": "reference", "us_per_layer_step": round(us, 2),
+        "sample": f"the reference's FloatTransformer::run_layer, {len(long_t)} calls each at pos {T - 1} and pos 0 "
+                  f"alternating over an engine of {n_l} layers (synthetic weights, sequence 0's device cache "
+                  f"rows); attention = difference of the medians ({float(np.median(long_t)) * 1e6:.1f} - "
+                  f"{float(np.median(short_t)) * 1e6:.1f} us); the reference's own OpenMP",
+    }
+
+
+def cpu_baseline(att, workload, Ts, n_layers_sample: int, budget_s: float):
+    """The reference's attention through its run_layer when oracle/_ref is
+    present and the workload uses the reference's fixed RoPE base; otherwise
+    the oracle on the host on layers [0, n_layers_sample) of sequence 0 of
+    the device cache (downloaded bytes), repeating sweeps for about budget_s
+    seconds."""
+    from oracle import oracle as O
+    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    if O.ref_available() and theta == 500000.0:
+        return cpu_baseline_reference(att, workload, int(Ts[0]), budget_s)
     if not os.path.isfile(O.ORACLE_SO):
         O.build(ref=False)
     env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
