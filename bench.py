@@ -352,6 +352,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="llama3-8b-ctx4096", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-host-pointer", action="store_true",
+                    help="skip the host-pointer (PCIe-inclusive) leg, e.g. under a profiler")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--split", type=int, default=0, help="positions per split-K chunk (0 = auto)")
@@ -514,7 +516,7 @@ def main():
         },
         "cpu_baseline": None,
     }
-    if batch == 1:
+    if batch == 1 and not args.no_host_pointer:
         result["host_pointer"] = host_pointer_rate(att, L, pos, bytes_layer, is_block,
                                                    sweeps=max(1, min(steps, 20)))
     if not args.no_cpu:
