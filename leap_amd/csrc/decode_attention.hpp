@@ -20,6 +20,12 @@
 //     into the output.  Each counter sees at most kSubGroup (or kMaxSub)
 //     arrivals and each fold reads a few KB, instead of one workgroup pulling
 //     every partial through a single CU.
+//   - when every CU runs two one-pass workgroups of the launch, a CU receives
+//     its data in issue order, so the first-dispatched half of a group's chunks
+//     finishes about half a stream earlier than the rest.  That half folds in
+//     sub-groups while the stream runs; the second half counts straight into
+//     the final counter, whose last arrival folds the second half's chunk
+//     records and the first half's sub-group records in one level.
 //
 // XCD placement.  Workgroups are dealt to the XCDs round-robin by workgroup
 // id, so id % 8 names the XCD (the same holds within a 1-, 2- or 4-XCD
@@ -34,6 +40,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace leap {
 
@@ -80,6 +88,8 @@ struct StepArgs {
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
+    int merge_asym;      // every CU runs two one-pass workgroups of the launch: the
+                         // first-dispatched half of a group's chunks finishes first
 };
 
 // ---- buffer access ------------------------------------------------------------
@@ -606,7 +616,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     float4 *mo = &comb_o[0][0][0][0];      // [GM][MG][D4]
     float *mmx = &p_lds[0][0];             // [GM][MG]
     float *mls = &p_lds[0][0] + GM * MG;   // [GM][MG]
-    constexpr int B = 8;  // records in flight per lane
+    constexpr int B = 8;    // records in flight per lane
+    constexpr int BW = 20;  // per lane in the one-level final fold of the asymmetric merge
     // Online fold of records first + c, c = c_begin, c_begin + step, ... < n,
     // into (oo, mm, ll): B records of loads in flight at a time (L2 reads).
     auto fold_lane = [&](int first, int c_begin, int step, int n, float4 &oo, float &mm, float &ll) {
@@ -636,6 +647,57 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
                 ll += w * mlb[j].y;
             }
             mm = m_new;
+        }
+    };
+    // Fold records [first, first + n), n <= MG * BW a compile-time count
+    // (std::integral_constant), as one batch of loads: record lane mg takes
+    // records mg, mg + MG, ..., and the lanes meet in LDS.  Leaves (ox, Mx,
+    // Lx) in the threads with mg == 0.  With n known, every load a lane
+    // issues is unconditional and exactly the records it needs.
+    auto fold_wide = [&](int first, auto n_c, float4 &ox, float &Mx, float &Lx) {
+        constexpr int n = decltype(n_c)::value;
+        static_assert(n <= MG * BW, "records per lane");
+        float2 mlb[BW];
+        float4 ob[BW];
+#pragma unroll
+        for (int j = 0; j < BW; j++) {
+            const int c = mg + j * MG;
+            const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
+            const bool in = live && c < n;
+            mlb[j] = buf_load2<kSc1>(wm_rsrc, in ? row * 8u : ws_ml_bytes);
+            ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
+        }
+        float mm = -INFINITY, ll = 0.f;
+        float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < BW; j++)
+            if (mg + j * MG < n) mm = fmaxf(mm, mlb[j].x);
+#pragma unroll
+        for (int j = 0; j < BW; j++) {
+            const float w = (mg + j * MG < n) ? fast_exp2(mlb[j].x - mm) : 0.f;
+            fma4(oo, w, ob[j]);
+            ll += w * mlb[j].y;
+        }
+        __syncthreads();  // LDS scratch is free
+        mo[(mh * MG + mg) * D4 + md4] = oo;
+        if (md4 == 0) {
+            mmx[mh * MG + mg] = mm;
+            mls[mh * MG + mg] = ll;
+        }
+        __syncthreads();
+        if (mg == 0) {
+            Mx = -INFINITY;
+#pragma unroll
+            for (int g = 0; g < MG; g++) Mx = fmaxf(Mx, mmx[mh * MG + g]);
+            Lx = 0.f;
+            ox = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int g = 0; g < MG; g++) {
+                const float mgv = mmx[mh * MG + g];
+                const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
+                fma4(ox, sc, mo[(mh * MG + g) * D4 + md4]);
+                Lx += sc * mls[mh * MG + g];
+            }
         }
     };
     // Fold records [first, first + n) of the G heads into (ox, Mx, Lx) of
@@ -679,6 +741,63 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     };
     int *ctr = a.counters + ((size_t)seq * a.n_kv_heads + kvh) * kCounters;
     float4 *out_row = reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD);
+
+    // The asymmetric merge (see the header), for NC chunks: chunks [0, NC/2)
+    // fold in sub-groups whose records go right after the chunk records, and
+    // the final fold reads records [NC/2, NC + NC/2/kSubGroup), one range.
+    // NC is compiled in (32, 48 or 64) so that the final fold's loads are
+    // exact.
+    auto merge_asym = [&](auto nc_c) {
+        constexpr int NC = decltype(nc_c)::value, half = NC / 2, n_final = half + half / kSubGroup;
+        if (chunk_id < half) {
+            const int sg1 = chunk_id / kSubGroup;
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0) {
+                const int prev = __hip_atomic_fetch_add(ctr + (1 + sg1) * kCtrStride, 1, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_WORKGROUP);
+                s_last = (prev == kSubGroup - 1);
+            }
+            __syncthreads();
+            if (!s_last) return;
+            if (tid == 0) ctr[(1 + sg1) * kCtrStride] = 0;
+            float4 o1;
+            float M1, L1;
+            fold(sg1 * kSubGroup, kSubGroup, o1, M1, L1);
+            if (mg == 0 && live) {
+                const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(NC + sg1);
+                buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, o1);
+                if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M1, L1));
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            s_last = (prev == n_final - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) ctr[0] = 0;
+        float4 of;
+        float Mf, Lf;
+        fold_wide(half, std::integral_constant<int, n_final>{}, of, Mf, Lf);
+        if (mg == 0 && live) {
+            scale4(of, 1.0f / Lf);
+            out_row[md4] = of;
+        }
+    };
+    if (a.merge_asym) {
+        if constexpr (32 + 4 <= MG * BW) {
+            if (n_chunks == 64) return merge_asym(std::integral_constant<int, 64>{});
+        }
+        if constexpr (24 + 3 <= MG * BW) {
+            if (n_chunks == 48) return merge_asym(std::integral_constant<int, 48>{});
+        }
+        if constexpr (16 + 2 <= MG * BW) {
+            if (n_chunks == 32) return merge_asym(std::integral_constant<int, 32>{});
+        }
+    }
 
     // Level 1: once this workgroup's partials have reached L2 (stores
     // drained), count it in on its sub-group's counter (an L2 atomic).

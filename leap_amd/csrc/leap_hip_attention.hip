@@ -198,6 +198,10 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     const long long n_groups = (long long)n_seq * h->cfg.n_kv_heads;
     const long long n_wg = (n_groups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
     if (n_wg > 0x7fffffffLL) return set_err(h, -EINVAL, "launch too large");
+    // One pass per workgroup and at least two workgroups per CU: a CU's
+    // second workgroup receives its rows after its first, so each group's
+    // first-dispatched half of chunks can fold while the rest streams.
+    a.merge_asym = (chunk == leap::rows_per_pass(hd, h->group, kWaves) && n_groups * grid_x >= 2LL * h->n_cu) ? 1 : 0;
     hipLaunchKernelGGL(fn, dim3((unsigned)n_wg), dim3(kThreads), 0, stream, a);
     HIP_TRY(h, hipGetLastError());
     return 0;

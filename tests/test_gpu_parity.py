@@ -81,7 +81,10 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
 
 @pytest.mark.parametrize("nh,nkv,hd", SHAPES)
 @pytest.mark.parametrize("T,split", [(1, 0), (2, 0), (64, 0), (65, 64), (300, 128), (1000, 64),
-                                     (2049, 0), (777, 256)])
+                                     (2049, 0), (777, 256),
+                                     # 32, 48 and 64 one-pass chunks: the asymmetric merge when the
+                                     # launch puts two workgroups on every CU
+                                     (2048, 64), (3072, 64), (4096, 64)])
 def test_step_shapes_and_splits(nh, nkv, hd, T, split):
     theta = 10000.0 if hd == 64 else 500000.0
     rng = rng_for(nh, nkv, hd, T, split)
