@@ -491,6 +491,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
 int leap_hip_attention_destroy(leap_hip_attention *h)
 {
     if (!h) return 0;
+    (void)hipSetDevice(h->cfg.device);  // the handle's device, as for every other call
     if (h->stream) (void)hipStreamSynchronize(h->stream);
     void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->in_dev,
                     h->out_dev, h->blk,     h->w_qkv, h->w_o,   h->w_rms, h->w8_qkv,   h->s8_qkv,
