@@ -288,3 +288,35 @@ def test_async_entry_points_on_a_torch_stream():
         with pytest.raises(LeapError):
             att.step_batched_async(0, 2, pos.data_ptr(), T - 1, bq.data_ptr(), bk.data_ptr(),
                                    bv.data_ptr(), hint.data_ptr(), s.cuda_stream, total_rows=2 * T + 1)
+
+
+def _random_cases(n, seed):
+    """Seeded draws over the supported space: head shape, context, forced
+    chunk size (0 = the automatic choice) and batch with ragged positions."""
+    shapes = [(32, 8, 128), (24, 8, 128), (16, 16, 64), (32, 4, 64), (64, 8, 128), (8, 8, 128),
+              (16, 2, 128), (12, 4, 64), (8, 1, 64), (4, 2, 64)]
+    rng = np.random.default_rng(seed)
+    for i in range(n):
+        nh, nkv, hd = shapes[rng.integers(len(shapes))]
+        T = int(rng.choice([rng.integers(1, 200), rng.integers(200, 5000)]))
+        split = int(rng.choice([0, 0, 64, 128, 192, 256, 512]))
+        batch = int(rng.choice([1, 1, 2, 5]))
+        yield pytest.param(nh, nkv, hd, T, split, batch, id=f"{i}-{nh}x{nkv}x{hd}-T{T}-s{split}-b{batch}")
+
+
+@pytest.mark.parametrize("nh,nkv,hd,T,split,batch", list(_random_cases(40, 0x51AB)))
+def test_random_shapes_positions_and_batches(nh, nkv, hd, T, split, batch):
+    """Seeded random cases beyond the fixed grid; a batch holds sequences at
+    ragged positions up to T - 1, the first at T - 1."""
+    rng = rng_for(nh, nkv, hd, T, split, batch, 77)
+    with HipAttention(nh, nkv, hd, T, max_batch=batch) as att:
+        att.kv_fill_normal(int(rng.integers(1 << 30)), 1.0 / np.sqrt(hd))
+        if split:
+            att.set_split(split)
+        pos = np.concatenate([[T - 1], rng.integers(0, T, size=batch - 1)]).astype(np.int32)
+        q = normal(rng, (batch, nh * hd), hd)
+        k = normal(rng, (batch, nkv * hd), hd)
+        v = normal(rng, (batch, nkv * hd), hd)
+        out = att.step(0, int(pos[0]), q[0], k[0], v[0])[None] if batch == 1 else att.step_batched(0, pos, q, k, v)
+        for i in range(batch):
+            _step_and_check(att, 0, int(pos[i]), q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
