@@ -857,6 +857,15 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x)
 }
 
 // Two N(0,1) values per counter (Box-Muller on two 24-bit uniforms).
+// Copy n16 16-byte words from device-accessible (pinned) host memory: the
+// host-pointer entry points stage their few KB of inputs this way, reading
+// across PCIe from the kernel instead of a DMA-engine copy.
+__global__ void stage_in_kernel(float4 *__restrict__ dst, const float4 *__restrict__ src, int n16)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) dst[i] = src[i];
+}
+
 __global__ void fill_normal_kernel(float *dst, size_t n, uint64_t seed, float scale)
 {
     const size_t stride = (size_t)gridDim.x * blockDim.x * 2;

@@ -308,7 +308,7 @@ Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
     return best->fn;
 }
 
-int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, hipStream_t stream)
+int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, float *x_res, hipStream_t stream)
 {
     const int dim = h->q_dim, kv = h->kv_dim, gs = h->gs;
     float *q = h->blk, *k = q + dim, *v = k + kv, *xb = v + kv;
@@ -340,7 +340,7 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     pa.x = xb;
     pa.w = h->w8_o + (size_t)li * dim * dim;
     pa.ws = h->s8_o + (size_t)li * dim * (dim / gs);
-    pa.out0 = x;
+    pa.out0 = x_res;
     pa.rows = dim;
     pa.n0 = dim;
     pa.xq_out = aq;
@@ -353,11 +353,13 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     return 0;
 }
 
-int launch_block(leap_hip_attention *h, int layer, int pos, float *x, hipStream_t stream)
+// x: the residual stream the q/k/v projection normalises; x_res: where the
+// wo product is added (x itself, or a device-accessible host copy of it).
+int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_res, hipStream_t stream)
 {
     const int li = layer - h->cfg.layer_begin;
     if (h->w_fmt == 0 || !h->w_set[li]) return set_err(h, -EINVAL, "no weights set for layer %d", layer);
-    if (h->w_fmt == 2) return launch_block_q8(h, li, layer, pos, x, stream);
+    if (h->w_fmt == 2) return launch_block_q8(h, li, layer, pos, x, x_res, stream);
     QkvFn qkv;
     ProjFn proj;
     int rb;
@@ -380,7 +382,7 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, hipStream_
     leap::ProjArgs pa{};
     pa.xb = xb;
     pa.w = h->w_o + (size_t)li * dim * dim;
-    pa.x = x;
+    pa.x = x_res;
     pa.d = dim;
     hipLaunchKernelGGL(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, pa);
     HIP_TRY(h, hipGetLastError());
@@ -474,7 +476,8 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters;
     CREATE_TRY(hipMalloc(&h->counters, n_ctr * sizeof(int)));
     CREATE_TRY(hipMemsetAsync(h->counters, 0, n_ctr * sizeof(int), h->stream));
-    h->in_bytes = (size_t)c.max_batch * ((h->q_dim + 2 * h->kv_dim) * sizeof(float) + sizeof(int));
+    // rounded up to 16 bytes: the inputs are staged in as 16-byte words
+    h->in_bytes = ((size_t)c.max_batch * ((h->q_dim + 2 * h->kv_dim) * sizeof(float) + sizeof(int)) + 15) / 16 * 16;
     CREATE_TRY(hipMalloc(&h->in_dev, h->in_bytes));
     CREATE_TRY(hipHostMalloc((void **)&h->in_host, h->in_bytes, hipHostMallocDefault));
     CREATE_TRY(hipHostMalloc((void **)&h->out_host, (size_t)c.max_batch * h->q_dim * sizeof(float),
@@ -538,12 +541,16 @@ int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const flo
     std::memcpy(h->in_host, q, qb);
     std::memcpy(h->in_host + qb, k_new, kb);
     std::memcpy(h->in_host + qb + kb, v_new, kb);
-    HIP_TRY(h, hipMemcpyAsync(h->in_dev, h->in_host, qb + 2 * kb, hipMemcpyHostToDevice, s));
+    const int n16 = (int)((qb + 2 * kb) / 16);
+    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16);
+    HIP_TRY(h, hipGetLastError());
     const float *qd = reinterpret_cast<const float *>(h->in_dev);
+    // The output goes straight to the pinned buffer (device-accessible host
+    // memory): the kernel's final stores cross PCIe, with no copy after it.
     if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, qd, qd + h->q_dim, qd + h->q_dim + h->kv_dim,
-                        h->out_dev, s))
+                        h->out_host, s))
         return rc;
-    HIP_TRY(h, hipMemcpyAsync(h->out_host, h->out_dev, qb, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
     std::memcpy(out, h->out_host, qb);
     return 0;
@@ -597,12 +604,14 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
     std::memcpy(h->in_host + qb, k_new, kb);
     std::memcpy(h->in_host + qb + kb, v_new, kb);
     std::memcpy(h->in_host + qb + 2 * kb, pos, n_seq * sizeof(int));
-    HIP_TRY(h, hipMemcpyAsync(h->in_dev, h->in_host, qb + 2 * kb + n_seq * sizeof(int), hipMemcpyHostToDevice, s));
+    const int n16 = (int)((qb + 2 * kb + n_seq * sizeof(int) + 15) / 16);  // in_bytes is a multiple of 16
+    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16);
+    HIP_TRY(h, hipGetLastError());
     const float *qd = reinterpret_cast<const float *>(h->in_dev);
     const float *kd = qd + (size_t)n_seq * h->q_dim, *vd = kd + (size_t)n_seq * h->kv_dim;
     const int *pd = reinterpret_cast<const int *>(h->in_dev + qb + 2 * kb);
-    if (int rc = launch(h, layer, n_seq, pd, 0, max_pos, rows, qd, kd, vd, h->out_dev, s)) return rc;
-    HIP_TRY(h, hipMemcpyAsync(h->out_host, h->out_dev, qb, hipMemcpyDeviceToHost, s));
+    if (int rc = launch(h, layer, n_seq, pd, 0, max_pos, rows, qd, kd, vd, h->out_host, s)) return rc;
     HIP_TRY(h, hipStreamSynchronize(s));
     std::memcpy(out, h->out_host, qb);
     return 0;
@@ -725,7 +734,7 @@ int leap_hip_attention_block_async(leap_hip_attention *h, int layer, int pos, fl
     if (!x) return set_err(h, -EINVAL, "NULL buffer");
     if (reinterpret_cast<uintptr_t>(x) % 16) return set_err(h, -EINVAL, "x must be 16-byte aligned");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
-    return launch_block(h, layer, pos, x, (hipStream_t)stream);
+    return launch_block(h, layer, pos, x, x, (hipStream_t)stream);
 }
 
 int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x)
@@ -739,9 +748,13 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
     hipStream_t s = h->stream;
     float *xd = h->blk + 2 * h->q_dim + 2 * h->kv_dim;
     const size_t xb = (size_t)h->q_dim * sizeof(float);
-    std::memcpy(h->out_host, x, xb);  // through pinned memory: one DMA each way
-    HIP_TRY(h, hipMemcpyAsync(xd, h->out_host, xb, hipMemcpyHostToDevice, s));
-    if (int rc = launch_block(h, layer, pos, xd, s)) return rc;
+    std::memcpy(h->out_host, x, xb);  // through pinned memory: staged in by a kernel, one DMA out
+    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((xb / 16 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<float4 *>(xd), reinterpret_cast<const float4 *>(h->out_host), (int)(xb / 16));
+    HIP_TRY(h, hipGetLastError());
+    if (int rc = launch_block(h, layer, pos, xd, xd, s)) return rc;
+    // (adding the wo product straight into the pinned copy measured slower:
+    // the residual reads cross PCIe on the wo kernel's critical path)
     HIP_TRY(h, hipMemcpyAsync(h->out_host, xd, xb, hipMemcpyDeviceToHost, s));
     HIP_TRY(h, hipStreamSynchronize(s));
     std::memcpy(x, h->out_host, xb);
