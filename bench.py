@@ -121,6 +121,29 @@ def quantize_groups(w: np.ndarray, gs: int):
     return q.reshape(w.shape), sc
 
 
+def hip_graph_us(one_step, stream, steps: int, n_layers: int) -> float:
+    """Microseconds per layer-step of one_step captured once into a HIP graph
+    (its launches only: the entry points enqueue kernels and nothing else)
+    and replayed `steps` times on `stream`."""
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        one_step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            graph.replay()
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (steps * n_layers)
+
+
 def traffic_from_profiles(workload: str):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE runs
     (scaled by a copy kernel's counters), recorded in profiles/."""
@@ -357,6 +380,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--split", type=int, default=0, help="positions per split-K chunk (0 = auto)")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay timing")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -469,6 +493,7 @@ def main():
 
     launches = steps * L
     us_layer = ms_total * 1e3 / launches
+    graph_us = None if args.no_graph else hip_graph_us(one_step, stream, steps, L)
     is_q8 = args.workload in Q8_WORKLOADS
     per_seq = q8_block_bytes if is_q8 else block_bytes if is_block else algorithmic_bytes
     bytes_layer = int(sum(per_seq(int(T), nh, nkv, hd) for T in Ts))
@@ -516,6 +541,13 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if graph_us is not None:
+        result["hip_graph"] = {
+            "us_per_layer_step": round(graph_us, 3),
+            "value": round(bytes_layer / (graph_us * 1e-6) / 1e9, 2),
+            "unit": "GB/s",
+            "note": "the same step captured once into a HIP graph and replayed; `value` above is eager launches",
+        }
     if batch == 1 and not args.no_host_pointer:
         result["host_pointer"] = host_pointer_rate(att, L, pos, bytes_layer, is_block,
                                                    sweeps=max(1, min(steps, 20)))
