@@ -479,17 +479,23 @@ def main():
         one_step()
     torch.cuda.synchronize()
 
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+    # The timed region, cut into up to 10 segments by events on the same
+    # stream (for the spread); the total runs from the first event to the last.
+    n_seg = min(10, steps)
+    bounds = [round(i * steps / n_seg) for i in range(n_seg + 1)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_seg + 1)]
     torch.cuda.synchronize()
-    ev0.record(stream)
+    evs[0].record(stream)
     t0 = time.perf_counter()
-    for _ in range(steps):
-        one_step()
-    ev1.record(stream)
+    for i in range(n_seg):
+        for _ in range(bounds[i + 1] - bounds[i]):
+            one_step()
+        evs[i + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_total = ev0.elapsed_time(ev1)
+    ms_total = evs[0].elapsed_time(evs[-1])
+    seg_us = np.array([evs[i].elapsed_time(evs[i + 1]) * 1e3 / ((bounds[i + 1] - bounds[i]) * L)
+                       for i in range(n_seg)])
 
     launches = steps * L
     us_layer = ms_total * 1e3 / launches
@@ -525,6 +531,9 @@ def main():
             {"min": int(Ts.min()), "max": int(Ts.max()), "sum": int(Ts.sum())},
         },
         "us_per_layer_step": round(us_layer, 3),
+        "us_per_layer_step_spread": {"segments": n_seg, "median": round(float(np.median(seg_us)), 3),
+                                     "p10": round(float(np.percentile(seg_us, 10)), 3),
+                                     "p90": round(float(np.percentile(seg_us, 90)), 3)},
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "tokens_layers_per_s": round(batch * 1e6 / us_layer, 1),
         "host_wall_s": round(wall, 4),
