@@ -82,7 +82,8 @@ const char *leap_hip_attention_last_error(const leap_hip_attention *h);
 int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const float *q,
                             const float *k_new, const float *v_new, float *out);
 
-/* As leap_hip_attention_step, with device pointers, enqueued on `stream`. */
+/* As leap_hip_attention_step, with device pointers, enqueued on `stream`.
+ * q, k_new, v_new and out must be 16-byte aligned (-EINVAL otherwise). */
 int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, const float *q,
                                   const float *k_new, const float *v_new, float *out,
                                   void *stream);
@@ -102,7 +103,9 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
  * seq_len are skipped and their outputs left unwritten.  total_rows is the
  * host's sum of pos[i] + 1 when it has one (it only steers the split of the
  * positions over workgroups), or 0 when it does not: the launch is then
- * sized as if the sequences were spread evenly up to max_pos. */
+ * sized as if the sequences were spread evenly up to max_pos.  q, k_new,
+ * v_new and out must be 16-byte aligned and pos 4-byte aligned (-EINVAL
+ * otherwise). */
 int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int n_seq,
                                           const int *pos, int max_pos, long long total_rows,
                                           const float *q, const float *k_new, const float *v_new,

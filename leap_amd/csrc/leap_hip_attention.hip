@@ -513,6 +513,10 @@ const char *leap_hip_attention_last_error(const leap_hip_attention *h)
     return h ? h->err.c_str() : g_create_error.c_str();
 }
 
+// The kernel reads q, k_new and v_new and writes out with 8- and 16-byte
+// vector accesses.
+static inline bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
 int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, const float *q,
                                   const float *k_new, const float *v_new, float *out,
                                   void *stream)
@@ -522,6 +526,8 @@ int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, con
     if (pos < 0 || pos >= h->cfg.seq_len)
         return set_err(h, -EINVAL, "pos %d outside [0, %d)", pos, h->cfg.seq_len);
     if (!q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(out))
+        return set_err(h, -EINVAL, "q, k_new, v_new and out must be 16-byte aligned");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     return launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k_new, v_new, out,
                   (hipStream_t)stream);
@@ -568,6 +574,9 @@ int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int 
     if (max_pos < 0 || max_pos >= h->cfg.seq_len)
         return set_err(h, -EINVAL, "max_pos %d outside [0, %d)", max_pos, h->cfg.seq_len);
     if (!pos || !q || !k_new || !v_new || !out) return set_err(h, -EINVAL, "NULL buffer");
+    if (!aligned16(q) || !aligned16(k_new) || !aligned16(v_new) || !aligned16(out) ||
+        reinterpret_cast<uintptr_t>(pos) % 4)
+        return set_err(h, -EINVAL, "q, k_new, v_new and out must be 16-byte aligned, pos 4-byte aligned");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     if (total_rows < 0 || total_rows > (long long)n_seq * (max_pos + 1))
         return set_err(h, -EINVAL, "total_rows %lld outside [0, %lld]", total_rows,

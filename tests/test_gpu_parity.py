@@ -269,6 +269,11 @@ def test_async_entry_points_on_a_torch_stream():
                        s.cuda_stream)
         s.synchronize()
         assert np.array_equal(dout.cpu().numpy(), ref)
+        # device pointers that are not 16-byte aligned are refused before any launch
+        for shift in ((4, 0, 0, 0), (0, 8, 0, 0), (0, 0, 4, 0), (0, 0, 0, 12)):
+            with pytest.raises(LeapError):
+                att.step_async(0, T - 1, dq.data_ptr() + shift[0], dk.data_ptr() + shift[1],
+                               dv.data_ptr() + shift[2], dout.data_ptr() + shift[3], s.cuda_stream)
         # batched async with device positions
         pos = torch.tensor([T - 1, 17], dtype=torch.int32, device="cuda")
         bq, bk, bv = (torch.stack([t, t]) for t in (dq, dk, dv))
