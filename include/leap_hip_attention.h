@@ -19,14 +19,25 @@
  * Conventions
  *   - Every entry point returns 0 on success or a negative errno value:
  *     -EINVAL bad argument, -ENOMEM allocation failure, -ENODEV no usable
- *     GPU, -EIO a HIP runtime error.  The message of the last failure on a
- *     handle is kept for leap_hip_attention_last_error.  Nothing throws across
- *     this boundary.
+ *     GPU, -ENOTSUP a device that does not place workgroups the way the
+ *     kernel's merge needs (checked at create), -EIO a HIP runtime error.
+ *     The message of the last failure on a handle is kept for
+ *     leap_hip_attention_last_error.  Nothing throws across this boundary.
  *   - A handle is used by one host thread at a time; distinct handles are
  *     independent.  Device work is ordered on a stream: the host-pointer
  *     entry points use the handle's own stream and return when results are
  *     in host memory; the _async entry points take device pointers and a
- *     hipStream_t (0 = the default stream) and return after enqueueing.
+ *     hipStream_t (0 = the legacy default stream) and return after
+ *     enqueueing.
+ *   - Every launch of a handle shares its caches, its split-K workspace and
+ *     its arrival counters, so launches of one handle must not overlap.  The
+ *     handle's own stream is ordered with the legacy default stream; after
+ *     _async calls on any other stream, synchronise that stream (or make the
+ *     next stream wait for it) before a host-pointer call, clear, a
+ *     kv_upload/kv_download, set_layer_weights*, load_checkpoint or
+ *     destroy, and before _async calls on a different stream.  Launches that
+ *     overlapped leave the counters inconsistent and later outputs wrong;
+ *     leap_hip_attention_clear resets them.
  *   - `layer` is the model's global layer index, as in the reference's layer
  *     loop (FloatTransformer.cpp:768-770); a handle holds the layers
  *     [layer_begin, layer_end).
@@ -70,7 +81,8 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
 int leap_hip_attention_destroy(leap_hip_attention *h);
 
 /* Message of the last failure on `h` ("" if none); with h == NULL, the last
- * failure of leap_hip_attention_create on this thread. */
+ * failure on this thread of a call made without a handle
+ * (leap_hip_attention_create, leap_hip_attention_xcc_map). */
 const char *leap_hip_attention_last_error(const leap_hip_attention *h);
 
 /* One token, one layer, sequence 0 (FloatTransformer.cpp:396-662).
@@ -111,7 +123,8 @@ int leap_hip_attention_step_batched_async(leap_hip_attention *h, int layer, int 
                                           const float *q, const float *k_new, const float *v_new,
                                           float *out, void *stream);
 
-/* clear_kv_cache (FloatTransformer.cpp:74-77): zero both caches. */
+/* clear_kv_cache (FloatTransformer.cpp:74-77): zero both caches (and the
+ * split-K merge's arrival counters). */
 int leap_hip_attention_clear(leap_hip_attention *h);
 
 /* Copy cache rows [pos_begin, pos_end) of (seq, layer) between host memory
@@ -283,6 +296,12 @@ typedef struct leap_hip_attention_block_views {
     const float *as;
 } leap_hip_attention_block_views;
 int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention_block_views *out);
+
+/* Placement diagnostic: launch n_wg workgroups of the decode kernel's size on
+ * `device` and write the XCD (XCC_ID) each ran on to xcc_out[n_wg].  The
+ * decode kernel's merge needs xcc_out[i] == xcc_out[i % 8] for every i;
+ * leap_hip_attention_create checks that and returns -ENOTSUP otherwise. */
+int leap_hip_attention_xcc_map(int device, int n_wg, int *xcc_out);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,7 @@ EXPORTS = (
     "leap_hip_attention_block_views_get", "leap_hip_attention_checkpoint_read",
     "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
     "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
+    "leap_hip_attention_xcc_map",
 )
 
 PACKET_HEADER_BYTES = 8
@@ -110,6 +111,7 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_packet_header.argtypes = [ctypes.c_char_p, ctypes.c_size_t, _I, _IP, _IP]
     L.leap_hip_attention_packet_upload.argtypes = [H, ctypes.c_char_p, ctypes.c_size_t, _P, _IP, _IP, _P]
     L.leap_hip_attention_packet_download.argtypes = [H, _P, _I, _I, _P, ctypes.c_size_t, _P]
+    L.leap_hip_attention_xcc_map.argtypes = [_I, _I, ctypes.POINTER(_I)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -140,6 +142,16 @@ def checkpoint_read(path) -> dict:
     if rc != 0:
         raise LeapError(rc, f"{path}: {'cannot read' if rc == -errno.EIO else 'not a LEAP checkpoint'}")
     return {n: getattr(c, n) for n, _ in Checkpoint._fields_}
+
+
+def xcc_map(n_wg: int, device: int = 0) -> np.ndarray:
+    """The XCD each of n_wg workgroups of the decode kernel's size ran on."""
+    lib = load_library()
+    out = np.empty(n_wg, np.int32)
+    rc = lib.leap_hip_attention_xcc_map(device, n_wg, out.ctypes.data_as(ctypes.POINTER(_I)))
+    if rc != 0:
+        raise LeapError(rc, lib.leap_hip_attention_last_error(None).decode())
+    return out
 
 
 def packet_header(packet: bytes, dim):

@@ -49,12 +49,18 @@ constexpr int kWave = 64;
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
 constexpr int kSubGroup = 8;              // chunks per first-level merge
 constexpr int kMaxSub = kMaxChunks / kSubGroup;
-constexpr int kRecords = kMaxChunks + kMaxSub;  // partial records per head
 constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
 constexpr int kCounters = (1 + kMaxSub) * kCtrStride;  // counter words per (sequence, KV head)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
+
+// Partial records per head of a launch with grid_chunks chunks per sequence:
+// one per chunk, then one per first-level sub-group.
+__host__ __device__ constexpr int records_per_head(int grid_chunks)
+{
+    return grid_chunks + (grid_chunks + kSubGroup - 1) / kSubGroup;
+}
 
 // Rows of one wave sub-tile: 16 (two MFMA row sets), i.e. 16 KiB of K and V
 // at head_dim 128, whatever the number of q heads per KV head.
@@ -73,9 +79,9 @@ struct StepArgs {
     float *v_cache;
     const float4 *rope;  // [seq_len][HD/4] of (cos_2i, sin_2i, cos_2i+1, sin_2i+1)
     const int *pos_dev;  // per-sequence positions, or nullptr -> pos_scalar
-    float *ws_o;         // [n_seq][n_heads][kRecords][HD] partial outputs: chunk
-                         // records, then first-level merge records
-    float2 *ws_ml;       // [n_seq][n_heads][kRecords] (max, sum) in log2 units
+    float *ws_o;         // [n_seq][n_heads][records_per_head(grid_chunks)][HD] partial
+                         // outputs: chunk records, then first-level merge records
+    float2 *ws_ml;       // [n_seq][n_heads][records_per_head(grid_chunks)] (max, sum), log2 units
     int *counters;       // [n_seq][n_kv_heads][kCounters] arrival counters (final,
                          // then one per sub-group, kCtrStride apart), zero between launches
     long long seq_stride;// floats between sequence slabs
@@ -568,9 +574,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 
     // Combine the waves: one float4 of one head per thread.
     const bool single = (n_chunks == 1);
-    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * kRecords;
-    const uint32_t ws_o_bytes = (uint32_t)G * kRecords * HD * 4u;
-    const uint32_t ws_ml_bytes = (uint32_t)G * kRecords * 8u;
+    const int n_rec = records_per_head(a.grid_chunks);
+    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * (size_t)n_rec;
+    const uint32_t ws_o_bytes = (uint32_t)(G * n_rec * HD) * 4u;
+    const uint32_t ws_ml_bytes = (uint32_t)(G * n_rec) * 8u;
     const __amdgpu_buffer_rsrc_t wo_rsrc = make_rsrc(a.ws_o + ws_head0 * HD, ws_o_bytes);
     const __amdgpu_buffer_rsrc_t wm_rsrc = make_rsrc(a.ws_ml + ws_head0, ws_ml_bytes);
     for (int idx = tid; idx < G * D4; idx += S::THREADS) {
@@ -592,7 +599,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + ch) * HD)[cd4] = o;
         } else {
             // Partial o and (max, sum), into this XCD's L2.
-            const uint32_t row = (uint32_t)ch * kRecords + (uint32_t)chunk_id;
+            const uint32_t row = (uint32_t)(ch * n_rec + chunk_id);
             buf_store4(wo_rsrc, row * (HD * 4u) + 16u * cd4, o);
             if (cd4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M, L));
         }
@@ -627,7 +634,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
             for (int j = 0; j < B; j++) {
                 const int c = c0 + j * step;
-                const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
+                const uint32_t row = (uint32_t)(mh * n_rec + first + c);
                 // past n: an offset at the end of the range reads 0
                 const bool in = live && c < n;
                 mlb[j] = buf_load2<kSc1>(wm_rsrc, in ? row * 8u : ws_ml_bytes);
@@ -662,7 +669,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int j = 0; j < BW; j++) {
             const int c = mg + j * MG;
-            const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(first + c);
+            const uint32_t row = (uint32_t)(mh * n_rec + first + c);
             const bool in = live && c < n;
             mlb[j] = buf_load2<kSc1>(wm_rsrc, in ? row * 8u : ws_ml_bytes);
             ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
@@ -765,7 +772,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             float M1, L1;
             fold(sg1 * kSubGroup, kSubGroup, o1, M1, L1);
             if (mg == 0 && live) {
-                const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(NC + sg1);
+                const uint32_t row = (uint32_t)(mh * n_rec + NC + sg1);
                 buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, o1);
                 if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M1, L1));
             }
@@ -824,7 +831,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         return;
     }
     if (mg == 0 && live) {
-        const uint32_t row = (uint32_t)mh * kRecords + (uint32_t)(kMaxChunks + sg);
+        const uint32_t row = (uint32_t)(mh * n_rec + a.grid_chunks + sg);
         buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, ox);
         if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(Mx, Lx));
     }
@@ -839,10 +846,25 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     __syncthreads();
     if (!s_last) return;
     if (tid == 0) ctr[0] = 0;
-    fold(kMaxChunks, n_sg, ox, Mx, Lx);
+    fold(a.grid_chunks, n_sg, ox, Mx, Lx);
     if (mg == 0 && live) {
         scale4(ox, 1.0f / Lx);
         out_row[md4] = ox;
+    }
+}
+
+// ---- placement probe ---------------------------------------------------------
+
+// The XCC (XCD) each workgroup runs on, from the hardware register XCC_ID
+// (bits 3:0): xcc[blockIdx.x].  The decode kernel's merge keeps a group's
+// partials in one XCD's L2 on the assumption that workgroup ids equal modulo
+// kXcds land on the same XCD; create checks that with this probe.
+__global__ void xcc_probe_kernel(int *xcc)
+{
+    if (threadIdx.x == 0) {
+        unsigned v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        xcc[blockIdx.x] = (int)(v & 0xFu);
     }
 }
 

@@ -43,6 +43,7 @@ struct leap_hip_attention {
     float *ws_o = nullptr;
     float2 *ws_ml = nullptr;
     int *counters = nullptr;
+    size_t counter_bytes = 0;
     // The host-pointer entry points stage their inputs through one pinned
     // host buffer and one device region (q rows | k rows | v rows | pos, packed
     // for the call's n_seq), so that each call makes one DMA in and one out.
@@ -71,12 +72,16 @@ struct leap_hip_attention {
     hipStream_t stream = nullptr;
     int split = 0;
     int n_cu = 256;  // compute units of the device
+    int max_chunks = 1;  // chunks per sequence the workspace holds records for
     std::string err;
 };
 
 namespace {
 
-thread_local std::string g_create_error;
+// The message of the last failure of a call made without a handle (create,
+// the placement map) on this thread: a fixed buffer, so that recording it
+// allocates nothing.
+thread_local char g_create_error[512];
 
 int set_err(leap_hip_attention *h, int code, const char *fmt, ...)
 {
@@ -88,7 +93,7 @@ int set_err(leap_hip_attention *h, int code, const char *fmt, ...)
     if (h)
         h->err = buf;
     else
-        g_create_error = buf;
+        std::memcpy(g_create_error, buf, sizeof buf);
     return code;
 }
 
@@ -126,6 +131,35 @@ int check_layer(leap_hip_attention *h, int layer)
 
 int round_up(int x, int q) { return (x + q - 1) / q * q; }
 
+// What sizes and places one decode-attention launch: the head shape, the
+// device's compute units, a forced chunk size (0 = automatic) and the most
+// chunks per sequence the workspace holds records for.
+struct LaunchShape {
+    int head_dim, group, n_heads, n_kv_heads, seq_len;
+    int n_cu;
+    int split;
+    int max_chunks;
+};
+
+// The device buffers of one launch (one layer): the cache slabs of sequence
+// 0 at this layer and the distance between sequences, the RoPE table, and
+// the split-K workspace (records_per_head(grid) records per head and
+// sequence, counters zero between launches).
+struct LaunchBuffers {
+    float *k_cache, *v_cache;
+    long long seq_stride;
+    const float4 *rope;
+    float *ws_o;
+    float2 *ws_ml;
+    int *counters;
+};
+
+LaunchShape shape_of(const leap_hip_attention *h)
+{
+    return LaunchShape{h->cfg.head_dim, h->group, h->cfg.n_heads, h->cfg.n_kv_heads, h->cfg.seq_len,
+                       h->n_cu, h->split, h->max_chunks};
+}
+
 // Positions per workgroup (chunk), from the size and shape of the launch:
 //   - small launches (K/V bytes up to kLatencyBytes) are latency-bound: two
 //     workgroups per CU, all resident at once, each one pass of its waves;
@@ -135,22 +169,23 @@ int round_up(int x, int q) { return (x + q - 1) / q * q; }
 //     about 12 workgroups per CU over the launch, so that the last ones to
 //     start are short.
 // The sequence length (the mean one when ragged) is cut into equal chunks,
-// rounded up to whole passes; at most kMaxChunks chunks per sequence.
+// rounded up to whole passes; at most s.max_chunks chunks per sequence.
 constexpr long long kLatencyBytes = 128ll << 20;
 
-int choose_chunk(const leap_hip_attention *h, int n_seq, long long total_rows, int max_T)
+int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
-    const int quantum = leap::rows_per_pass(h->cfg.head_dim, h->group, kWaves);
-    const int floor_chunk = round_up((max_T + leap::kMaxChunks - 1) / leap::kMaxChunks, quantum);
+    const int quantum = leap::rows_per_pass(s.head_dim, s.group, kWaves);
+    const int floor_chunk = round_up((max_T + s.max_chunks - 1) / s.max_chunks, quantum);
+    const long long kv_dim = (long long)s.n_kv_heads * s.head_dim;
     int c;
-    if (h->split > 0) {
-        c = round_up(h->split, quantum);
+    if (s.split > 0) {
+        c = round_up(s.split, quantum);
     } else {
-        const long long bytes = total_rows * h->kv_dim * 8ll;
+        const long long bytes = total_rows * kv_dim * 8ll;
         const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
         const long long per_cu = bytes <= kLatencyBytes ? 2 : ragged ? 12 : 1;
-        const long long n_groups = (long long)n_seq * h->cfg.n_kv_heads;
-        const long long want_wgs = std::max<long long>(1, per_cu * h->n_cu);
+        const long long n_groups = (long long)n_seq * s.n_kv_heads;
+        const long long want_wgs = std::max<long long>(1, per_cu * s.n_cu);
         const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
         const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
         c = round_up((int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20), quantum);
@@ -159,51 +194,74 @@ int choose_chunk(const leap_hip_attention *h, int n_seq, long long total_rows, i
     return std::max(c, std::max(floor_chunk, quantum));
 }
 
-int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
-           int max_pos, long long total_rows, const float *q, const float *k, const float *v,
-           float *out, hipStream_t stream)
+// Most chunks per sequence any launch of a handle can make, for sizing its
+// workspace: every chunk is at least one pass of rows.
+int max_chunks_for(int seq_len, int head_dim, int group, int cap)
 {
-    const int hd = h->cfg.head_dim;
-    KernelFn fn = pick_kernel(hd, h->group);
-    if (!fn) return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", hd, h->group);
-    const int chunk = choose_chunk(h, n_seq, total_rows, max_pos + 1);
+    const int quantum = leap::rows_per_pass(head_dim, group, kWaves);
+    return std::max(1, std::min(cap, (seq_len + quantum - 1) / quantum));
+}
+
+// Enqueue one decode-attention launch.  Returns 0, or a HIP error code
+// (hipErrorInvalidValue for a shape without a kernel or a launch too large).
+hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_seq, const int *pos_dev,
+                            int pos_scalar, int max_pos, long long total_rows, const float *q, const float *k,
+                            const float *v, float *out, hipStream_t stream)
+{
+    const int hd = s.head_dim;
+    KernelFn fn = pick_kernel(hd, s.group);
+    if (!fn) return hipErrorInvalidValue;
+    const int chunk = choose_chunk(s, n_seq, total_rows, max_pos + 1);
     const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
+    if (grid_x > s.max_chunks) return hipErrorInvalidValue;
 
     leap::StepArgs a{};
     a.q = q;
     a.k_new = k;
     a.v_new = v;
     a.out = out;
-    const size_t loff = (size_t)(layer - h->cfg.layer_begin) * h->layer_floats;
-    a.k_cache = h->k_cache + loff;
-    a.v_cache = h->v_cache + loff;
-    a.rope = h->rope;
+    a.k_cache = b.k_cache;
+    a.v_cache = b.v_cache;
+    a.rope = b.rope;
     a.pos_dev = pos_dev;
-    a.ws_o = h->ws_o;
-    a.ws_ml = h->ws_ml;
-    a.counters = h->counters;
-    a.seq_stride = (long long)h->slab_floats;
+    a.ws_o = b.ws_o;
+    a.ws_ml = b.ws_ml;
+    a.counters = b.counters;
+    a.seq_stride = b.seq_stride;
     a.pos_scalar = pos_scalar;
     a.max_pos = max_pos;
-    a.seq_len = h->cfg.seq_len;
-    a.n_heads = h->cfg.n_heads;
-    a.n_kv_heads = h->cfg.n_kv_heads;
+    a.seq_len = s.seq_len;
+    a.n_heads = s.n_heads;
+    a.n_kv_heads = s.n_kv_heads;
     a.chunk = chunk;
     a.grid_chunks = grid_x;
-    a.n_groups = n_seq * h->cfg.n_kv_heads;
+    a.n_groups = n_seq * s.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
 
     // Workgroup id = ((group / 8) * grid_x + chunk) * 8 + group % 8, with
     // group = seq * n_kv_heads + kv_head: a group's chunks share one XCD.
-    const long long n_groups = (long long)n_seq * h->cfg.n_kv_heads;
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
     const long long n_wg = (n_groups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
-    if (n_wg > 0x7fffffffLL) return set_err(h, -EINVAL, "launch too large");
+    if (n_wg > 0x7fffffffLL) return hipErrorInvalidValue;
     // One pass per workgroup and at least two workgroups per CU: a CU's
     // second workgroup receives its rows after its first, so each group's
     // first-dispatched half of chunks can fold while the rest streams.
-    a.merge_asym = (chunk == leap::rows_per_pass(hd, h->group, kWaves) && n_groups * grid_x >= 2LL * h->n_cu) ? 1 : 0;
+    a.merge_asym = (chunk == leap::rows_per_pass(hd, s.group, kWaves) && n_groups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
     hipLaunchKernelGGL(fn, dim3((unsigned)n_wg), dim3(kThreads), 0, stream, a);
-    HIP_TRY(h, hipGetLastError());
+    return hipGetLastError();
+}
+
+int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
+           int max_pos, long long total_rows, const float *q, const float *k, const float *v,
+           float *out, hipStream_t stream)
+{
+    if (!pick_kernel(h->cfg.head_dim, h->group))
+        return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", h->cfg.head_dim, h->group);
+    const size_t loff = (size_t)(layer - h->cfg.layer_begin) * h->layer_floats;
+    const LaunchBuffers b{h->k_cache + loff, h->v_cache + loff, (long long)h->slab_floats, h->rope,
+                          h->ws_o,           h->ws_ml,          h->counters};
+    HIP_TRY(h, launch_attention(shape_of(h), b, n_seq, pos_dev, pos_scalar, max_pos, total_rows, q, k, v, out,
+                                stream));
     return 0;
 }
 
@@ -389,9 +447,49 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_r
     return 0;
 }
 
+// Run the XCC probe over n_wg workgroups of the decode kernel's block size
+// on `device` and copy the XCC id of each to xcc_host[n_wg].
+int xcc_map(leap_hip_attention *h, int device, int n_wg, int *xcc_host)
+{
+    HIP_TRY(h, hipSetDevice(device));
+    int *d = nullptr;
+    HIP_TRY(h, hipMalloc(&d, (size_t)n_wg * sizeof(int)));
+    hipLaunchKernelGGL(leap::xcc_probe_kernel, dim3((unsigned)n_wg), dim3(kThreads), 0, nullptr, d);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpy(xcc_host, d, (size_t)n_wg * sizeof(int), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return set_err(h, -EIO, "XCC probe: %s", hipGetErrorString(e));
+    return 0;
+}
+
+// The decode kernel's merge needs every workgroup whose id is equal modulo
+// kXcds on one XCD (one L2).  Check it on a launch of n_wg workgroups:
+// -ENOTSUP, with a message, when the device deals workgroups otherwise.
+int check_placement(leap_hip_attention *h, int device, int n_wg)
+{
+    std::vector<int> xcc((size_t)n_wg);
+    if (int rc = xcc_map(h, device, n_wg, xcc.data())) return rc;
+    for (int i = leap::kXcds; i < n_wg; i++)
+        if (xcc[i] != xcc[i % leap::kXcds])
+            return set_err(h, -ENOTSUP,
+                           "device %d placed workgroup %d on XCD %d and workgroup %d on XCD %d: the split-K "
+                           "merge needs workgroup ids equal modulo %d on one XCD",
+                           device, i, xcc[i], i % leap::kXcds, xcc[i % leap::kXcds], leap::kXcds);
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int leap_hip_attention_xcc_map(int device, int n_wg, int *xcc_out)
+{
+    if (!xcc_out || n_wg <= 0 || n_wg > (1 << 20)) return set_err(nullptr, -EINVAL, "bad probe arguments");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return set_err(nullptr, -ENODEV, "no HIP device");
+    if (device < 0 || device >= ndev) return set_err(nullptr, -EINVAL, "device %d of %d", device, ndev);
+    return xcc_map(nullptr, device, n_wg, xcc_out);
+}
 
 int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_attention **out)
 {
@@ -439,7 +537,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     h->slab_floats = (size_t)h->n_local * h->layer_floats;
 
     auto fail = [&](int rc) {
-        g_create_error = h->err;
+        std::snprintf(g_create_error, sizeof g_create_error, "%s", h->err.c_str());
         leap_hip_attention_destroy(h);
         return rc;
     };
@@ -451,7 +549,12 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
 
     CREATE_TRY(hipSetDevice(c.device));
     CREATE_TRY(hipDeviceGetAttribute(&h->n_cu, hipDeviceAttributeMultiprocessorCount, c.device));
-    CREATE_TRY(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+    // The handle's own stream (host-pointer calls, clear, transfers) is a
+    // blocking stream: it is ordered with work the caller enqueues on the
+    // legacy default stream (stream 0); other caller streams must be
+    // synchronised by the caller first.
+    CREATE_TRY(hipStreamCreate(&h->stream));
+    if (int prc = check_placement(h, c.device, 2 * h->n_cu)) return fail(prc);
     const size_t cache_bytes = (size_t)c.max_batch * h->slab_floats * sizeof(float);
     CREATE_TRY(hipMalloc(&h->k_cache, cache_bytes));
     CREATE_TRY(hipMalloc(&h->v_cache, cache_bytes));
@@ -470,12 +573,13 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMemcpyAsync(h->rope, packed.data(), packed.size() * sizeof(float),
                               hipMemcpyHostToDevice, h->stream));
 
-    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::kRecords;
+    h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, h->group, leap::kMaxChunks);
+    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    const size_t n_ctr = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters;
-    CREATE_TRY(hipMalloc(&h->counters, n_ctr * sizeof(int)));
-    CREATE_TRY(hipMemsetAsync(h->counters, 0, n_ctr * sizeof(int), h->stream));
+    h->counter_bytes = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters * sizeof(int);
+    CREATE_TRY(hipMalloc(&h->counters, h->counter_bytes));
+    CREATE_TRY(hipMemsetAsync(h->counters, 0, h->counter_bytes, h->stream));
     // rounded up to 16 bytes: the inputs are staged in as 16-byte words
     h->in_bytes = ((size_t)c.max_batch * ((h->q_dim + 2 * h->kv_dim) * sizeof(float) + sizeof(int)) + 15) / 16 * 16;
     CREATE_TRY(hipMalloc(&h->in_dev, h->in_bytes));
@@ -510,7 +614,7 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
 
 const char *leap_hip_attention_last_error(const leap_hip_attention *h)
 {
-    return h ? h->err.c_str() : g_create_error.c_str();
+    return h ? h->err.c_str() : g_create_error;
 }
 
 // The kernel reads q, k_new and v_new and writes out with 8- and 16-byte
@@ -833,6 +937,10 @@ int leap_hip_attention_clear(leap_hip_attention *h)
     const size_t bytes = (size_t)h->cfg.max_batch * h->slab_floats * sizeof(float);
     HIP_TRY(h, hipMemsetAsync(h->k_cache, 0, bytes, h->stream));
     HIP_TRY(h, hipMemsetAsync(h->v_cache, 0, bytes, h->stream));
+    // The merge's arrival counters too: they are zero between launches, and
+    // clearing them lets a handle recover after launches that overlapped on
+    // two streams.
+    HIP_TRY(h, hipMemsetAsync(h->counters, 0, h->counter_bytes, h->stream));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     return 0;
 }

@@ -79,3 +79,12 @@ def test_python_binding_raises_leaperror():
     with pytest.raises(A.LeapError) as ei:
         A.HipAttention(n_heads=8, n_kv_heads=3, head_dim=128, seq_len=16)
     assert ei.value.code == -errno.EINVAL
+
+
+def test_xcc_map_argument_checks():
+    lib = A.load_library()
+    buf = (ctypes.c_int * 8)()
+    assert lib.leap_hip_attention_xcc_map(0, 0, buf) == -errno.EINVAL
+    assert lib.leap_hip_attention_xcc_map(0, 8, None) == -errno.EINVAL
+    if not gpu_available():
+        assert lib.leap_hip_attention_xcc_map(0, 8, buf) == -errno.ENODEV

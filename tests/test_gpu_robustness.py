@@ -1,0 +1,95 @@
+"""Device placement, allocation failure and stream-ordering rules of the
+library, on the GPU, through the C ABI.
+
+- The split-K merge keeps a (sequence, KV head) group's partials in one XCD's
+  L2, which needs every workgroup id equal modulo 8 on the same XCD; create
+  checks that with a probe launch, and the probe's map is checked here too.
+- A create that runs out of device memory part-way returns -ENOMEM and frees
+  what it had already allocated; a normal create then succeeds.
+- After _async steps on a caller stream that the caller synchronised, the
+  handle's own calls (clear, host-pointer step) see their results, and clear
+  zeroes the cache rows and the merge counters.
+"""
+import errno
+
+import numpy as np
+import pytest
+
+from leap_amd import attention as A
+from leap_amd.attention import HipAttention, LeapError
+from oracle import oracle as O
+from tests.helpers import REL_TOL, assert_close, normal, rng_for
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _needs_gpu(hip_device):
+    return hip_device
+
+
+@pytest.mark.parametrize("n_wg", [8, 512, 4096])
+def test_xcc_map_is_periodic_in_eight(n_wg):
+    xcc = A.xcc_map(n_wg)
+    assert xcc.shape == (n_wg,)
+    assert ((xcc >= 0) & (xcc < 16)).all()
+    first = xcc[:min(8, n_wg)]
+    for i in range(8, n_wg):
+        assert xcc[i] == first[i % 8], f"workgroup {i} on XCD {xcc[i]}, workgroup {i % 8} on {first[i % 8]}"
+
+
+def test_oversize_create_returns_enomem_and_frees_everything():
+    import torch
+    torch.cuda.synchronize()
+    free0, total = torch.cuda.mem_get_info()
+    # each cache slab of 32 layers x 131072 positions x 1024 floats is 16 GiB;
+    # size the key cache at ~60% of free memory, so that it succeeds and the
+    # value cache of the same size does not
+    per_seq = 32 * 131072 * 1024 * 4
+    max_batch = int(0.6 * free0 // per_seq) + 1
+    assert 2 * max_batch * per_seq > free0
+    with pytest.raises(LeapError) as ei:
+        HipAttention(32, 8, 128, 131072, n_layers=32, max_batch=max_batch)
+    assert ei.value.code == -errno.ENOMEM, str(ei.value)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert abs(free1 - free0) <= 64 << 20, f"free memory {free0} before, {free1} after the failed create"
+    # a normal handle still works
+    rng = rng_for(91)
+    with HipAttention(8, 2, 128, 64) as att:
+        q, k, v = normal(rng, 8 * 128, 128), normal(rng, 256, 128), normal(rng, 256, 128)
+        out = att.step(0, 0, q, k, v)
+    assert np.array_equal(out.reshape(8, 128), np.repeat(v.reshape(2, 1, 128), 4, axis=1).reshape(8, 128))
+
+
+def test_async_on_a_caller_stream_then_clear_and_step():
+    import torch
+    nh, nkv, hd, T = 32, 8, 128, 4096
+    rng = rng_for(92)
+    with HipAttention(nh, nkv, hd, T) as att:
+        att.kv_fill_normal(92, 1.0 / np.sqrt(hd))
+        dev = torch.device("cuda:0")
+        s = torch.cuda.Stream()
+        q = torch.randn(nh * hd, device=dev) / np.sqrt(hd)
+        k = torch.randn(nkv * hd, device=dev) / np.sqrt(hd)
+        v = torch.randn(nkv * hd, device=dev) / np.sqrt(hd)
+        out = torch.empty(nh * hd, device=dev)
+        with torch.cuda.stream(s):
+            for pos in (4095, 2047, 63, 4095):  # multi-chunk merges on the caller's stream
+                att.step_async(0, pos, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        att.clear()
+        kz, vz = att.kv_download(0, 0, 0, T)
+        assert not kz.any() and not vz.any(), "clear left non-zero cache rows"
+        kr, vr = normal(rng, (3000, nkv * hd), hd), normal(rng, (3000, nkv * hd), hd)
+        att.kv_upload(0, 0, 0, kr, vr)
+        qh, kh, vh = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+        got = att.step(0, 3000, qh, kh, vh)
+        orc = O.Oracle(1, nh, nkv, hd, T)
+        orc.key_cache[0, :3000] = kr
+        orc.value_cache[0, :3000] = vr
+        want, _ = orc.step(0, 3000, qh, kh, vh)
+        assert_close(got, want, rel=REL_TOL)
+        k_slot, v_slot = att.kv_download(0, 0, 3000, 3001)
+        assert np.array_equal(k_slot[0], orc.key_cache[0, 3000])
+        assert np.array_equal(v_slot[0], orc.value_cache[0, 3000])
