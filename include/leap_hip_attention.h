@@ -82,7 +82,8 @@ int leap_hip_attention_destroy(leap_hip_attention *h);
 
 /* Message of the last failure on `h` ("" if none); with h == NULL, the last
  * failure on this thread of a call made without a handle
- * (leap_hip_attention_create, leap_hip_attention_xcc_map). */
+ * (leap_hip_attention_create, leap_hip_attention_step_noalloc,
+ * leap_hip_attention_xcc_map). */
 const char *leap_hip_attention_last_error(const leap_hip_attention *h);
 
 /* One token, one layer, sequence 0 (FloatTransformer.cpp:396-662).
@@ -135,6 +136,32 @@ int leap_hip_attention_kv_upload(leap_hip_attention *h, int seq, int layer, int 
                                  int pos_end, const float *k, const float *v);
 int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, int pos_begin,
                                    int pos_end, float *k, float *v);
+
+/* The attention step of leap_hip_attention_step_async for one sequence on
+ * caller-owned device buffers, allocating nothing: no handle, no hipMalloc,
+ * no allocating library call.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  The split-K workspace is
+ * a 4 MiB static device array, one per device (held until the process ends):
+ * a fixed 144 KiB region of arrival counters (n_kv_heads <= 128), then
+ * n_heads x 72 partial records of (head_dim + 2) floats, at most 64 split-K
+ * chunks per call (up to 108 heads of 128 or 212 heads of 64; Llama-3-8B
+ * uses 1.35 MB, Llama-3-70B 2.54 MB); larger shapes return -EINVAL.  Every
+ * call on one device shares that array: launches leave the counters at
+ * zero and the first call on a device clears the array on its stream, so
+ * calls that overlap on one GPU, on any streams, race.
+ *   cfg      n_heads, n_kv_heads, head_dim, seq_len and device are read
+ *   rope     [seq_len][head_dim/2] (cos, sin) pairs, fp32 (the reference's
+ *            rope_cos / rope_sin, FloatTransformer.cpp:56-72, interleaved)
+ *   k_cache, v_cache  this layer's cache rows of the sequence,
+ *            [seq_len][kv_dim] (FloatTransformer.cpp:396-398); row pos is
+ *            written (rotated k, v)
+ *   q, k_new, v_new, out   as leap_hip_attention_step_async
+ * Device pointers, all 16-byte aligned; enqueued on `stream`.  Failures
+ * are reported by leap_hip_attention_last_error(NULL). */
+int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int pos, const float *rope,
+                                    float *k_cache, float *v_cache, const float *q, const float *k_new,
+                                    const float *v_new, float *out, void *stream);
 
 /* ---- The attention sub-block of run_layer on the device ----------------- */
 

@@ -36,7 +36,7 @@ EXPORTS = (
     "leap_hip_attention_block_views_get", "leap_hip_attention_checkpoint_read",
     "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
     "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
-    "leap_hip_attention_xcc_map",
+    "leap_hip_attention_xcc_map", "leap_hip_attention_step_noalloc",
 )
 
 PACKET_HEADER_BYTES = 8
@@ -112,6 +112,7 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_packet_upload.argtypes = [H, ctypes.c_char_p, ctypes.c_size_t, _P, _IP, _IP, _P]
     L.leap_hip_attention_packet_download.argtypes = [H, _P, _I, _I, _P, ctypes.c_size_t, _P]
     L.leap_hip_attention_xcc_map.argtypes = [_I, _I, ctypes.POINTER(_I)]
+    L.leap_hip_attention_step_noalloc.argtypes = [ctypes.POINTER(Config), _I] + [_P] * 8
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
@@ -152,6 +153,18 @@ def xcc_map(n_wg: int, device: int = 0) -> np.ndarray:
     if rc != 0:
         raise LeapError(rc, lib.leap_hip_attention_last_error(None).decode())
     return out
+
+
+def step_noalloc(n_heads, n_kv_heads, head_dim, seq_len, pos, rope_ptr, k_cache_ptr, v_cache_ptr, q_ptr,
+                 k_ptr, v_ptr, out_ptr, stream=0, device=0):
+    """leap_hip_attention_step_noalloc on caller-owned device buffers (raw
+    addresses): no handle and no device allocation."""
+    lib = load_library()
+    cfg = Config(1, 0, 1, n_heads, n_kv_heads, head_dim, seq_len, 0.0, 1, device)
+    rc = lib.leap_hip_attention_step_noalloc(ctypes.byref(cfg), pos, rope_ptr, k_cache_ptr, v_cache_ptr, q_ptr,
+                                             k_ptr, v_ptr, out_ptr, stream)
+    if rc != 0:
+        raise LeapError(rc, lib.leap_hip_attention_last_error(None).decode())
 
 
 def packet_header(packet: bytes, dim):

@@ -17,8 +17,8 @@
 //     sub-group's counter (kSubGroup consecutive chunks); the last arrival of a
 //     sub-group folds that sub-group's partials into one record and counts in
 //     on the final counter, whose last arrival folds the sub-group records
-//     into the output.  Each counter sees at most kSubGroup (or kMaxSub)
-//     arrivals and each fold reads a few KB, instead of one workgroup pulling
+//     into the output.  Each counter sees at most kSubGroup (or
+//     kMaxChunks / kSubGroup) arrivals and each fold reads a few KB, instead of one workgroup pulling
 //     every partial through a single CU.
 //   - when every CU runs two one-pass workgroups of the launch, a CU receives
 //     its data in issue order, so the first-dispatched half of a group's chunks
@@ -48,9 +48,7 @@ namespace leap {
 constexpr int kWave = 64;
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
 constexpr int kSubGroup = 8;              // chunks per first-level merge
-constexpr int kMaxSub = kMaxChunks / kSubGroup;
 constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
-constexpr int kCounters = (1 + kMaxSub) * kCtrStride;  // counter words per (sequence, KV head)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
@@ -60,6 +58,15 @@ constexpr int kNt = 2;                    // cache policy nt: streamed once (the
 __host__ __device__ constexpr int records_per_head(int grid_chunks)
 {
     return grid_chunks + (grid_chunks + kSubGroup - 1) / kSubGroup;
+}
+
+// Counter words per (sequence, KV head) of a launch with grid_chunks chunks
+// per sequence: the final counter, then one per first-level sub-group, each
+// on its own 128-byte line.  Every counter is zero between launches, so
+// launches of different sizes may lay them out differently.
+__host__ __device__ constexpr int counters_per_group(int grid_chunks)
+{
+    return (1 + (grid_chunks + kSubGroup - 1) / kSubGroup) * kCtrStride;
 }
 
 // Rows of one wave sub-tile: 16 (two MFMA row sets), i.e. 16 KiB of K and V
@@ -82,8 +89,9 @@ struct StepArgs {
     float *ws_o;         // [n_seq][n_heads][records_per_head(grid_chunks)][HD] partial
                          // outputs: chunk records, then first-level merge records
     float2 *ws_ml;       // [n_seq][n_heads][records_per_head(grid_chunks)] (max, sum), log2 units
-    int *counters;       // [n_seq][n_kv_heads][kCounters] arrival counters (final,
-                         // then one per sub-group, kCtrStride apart), zero between launches
+    int *counters;       // [n_seq][n_kv_heads][counters_per_group(grid_chunks)] arrival
+                         // counters (final, then one per sub-group, kCtrStride apart),
+                         // zero between launches
     long long seq_stride;// floats between sequence slabs
     int pos_scalar;
     int max_pos;         // launch was sized for positions <= max_pos
@@ -746,7 +754,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             }
         }
     };
-    int *ctr = a.counters + ((size_t)seq * a.n_kv_heads + kvh) * kCounters;
+    int *ctr = a.counters + ((size_t)seq * a.n_kv_heads + kvh) * (size_t)counters_per_group(a.grid_chunks);
     float4 *out_row = reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD);
 
     // The asymmetric merge (see the header), for NC chunks: chunks [0, NC/2)

@@ -15,6 +15,7 @@
 #include <cstdio>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 #include <new>
 #include <string>
 #include <utility>
@@ -97,13 +98,32 @@ int set_err(leap_hip_attention *h, int code, const char *fmt, ...)
     return code;
 }
 
+// A failed HIP call also leaves its code as the thread's sticky "last
+// error"; it is read (cleared) here so that it cannot be reported again by a
+// later, unrelated query.
 #define HIP_TRY(h, call)                                                                       \
     do {                                                                                       \
         hipError_t e_ = (call);                                                                \
-        if (e_ != hipSuccess)                                                                  \
+        if (e_ != hipSuccess) {                                                                \
+            (void)hipGetLastError();                                                           \
             return set_err((h), e_ == hipErrorOutOfMemory ? -ENOMEM : -EIO, "%s: %s", #call,  \
                            hipGetErrorString(e_));                                             \
+        }                                                                                      \
     } while (0)
+
+template <typename T>
+struct same_type {
+    using type = T;
+};
+
+// Enqueue fn<<<grid, block, 0, stream>>>(args...) and return that launch's
+// own status (not the thread's sticky last error, which may be older).
+template <typename... P>
+hipError_t launch_k(void (*fn)(P...), dim3 grid, dim3 block, hipStream_t stream, typename same_type<P>::type... args)
+{
+    void *kargs[] = {static_cast<void *>(&args)...};
+    return hipLaunchKernel(reinterpret_cast<const void *>(fn), grid, block, kargs, 0, stream);
+}
 
 using KernelFn = void (*)(leap::StepArgs);
 
@@ -247,8 +267,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     // second workgroup receives its rows after its first, so each group's
     // first-dispatched half of chunks can fold while the rest streams.
     a.merge_asym = (chunk == leap::rows_per_pass(hd, s.group, kWaves) && n_groups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
-    hipLaunchKernelGGL(fn, dim3((unsigned)n_wg), dim3(kThreads), 0, stream, a);
-    return hipGetLastError();
+    return launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
 }
 
 int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
@@ -275,6 +294,7 @@ int alloc_all(leap_hip_attention *h, std::initializer_list<std::pair<void **, si
         void *p = nullptr;
         const hipError_t e = hipMalloc(&p, b.second);
         if (e != hipSuccess) {
+            (void)hipGetLastError();
             for (void *q : made) (void)hipFree(q);
             return set_err(h, e == hipErrorOutOfMemory ? -ENOMEM : -EIO, "hipMalloc(%zu bytes): %s", b.second,
                            hipGetErrorString(e));
@@ -388,9 +408,7 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     Q8Fn fn = pick_q8(dim, gs, leap::kQ8InRms, (int)rows_qkv, h->n_cu, &rpt);
     if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     int per_wg = leap::kQ8Teams * rpt;
-    hipLaunchKernelGGL(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream,
-                       qa);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, qa));
     int8_t *aq = h->q8_act + dim;
     float *as = h->q8_act_s + dim / gs;
     if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
@@ -406,8 +424,7 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     fn = pick_q8(dim, gs, leap::kQ8InF32, dim, h->n_cu, &rpt);
     if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     per_wg = leap::kQ8Teams * rpt;
-    hipLaunchKernelGGL(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), 0, stream, pa);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, pa));
     return 0;
 }
 
@@ -434,16 +451,14 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_r
     qa.v = v;
     qa.dim = dim;
     qa.kv_dim = kv;
-    hipLaunchKernelGGL(qkv, dim3((unsigned)((dim + 2 * kv + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, qa);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(qkv, dim3((unsigned)((dim + 2 * kv + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, qa));
     if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
     leap::ProjArgs pa{};
     pa.xb = xb;
     pa.w = h->w_o + (size_t)li * dim * dim;
     pa.x = x_res;
     pa.d = dim;
-    hipLaunchKernelGGL(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), 0, stream, pa);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, pa));
     return 0;
 }
 
@@ -454,11 +469,13 @@ int xcc_map(leap_hip_attention *h, int device, int n_wg, int *xcc_host)
     HIP_TRY(h, hipSetDevice(device));
     int *d = nullptr;
     HIP_TRY(h, hipMalloc(&d, (size_t)n_wg * sizeof(int)));
-    hipLaunchKernelGGL(leap::xcc_probe_kernel, dim3((unsigned)n_wg), dim3(kThreads), 0, nullptr, d);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_k(leap::xcc_probe_kernel, dim3((unsigned)n_wg), dim3(kThreads), nullptr, d);
     if (e == hipSuccess) e = hipMemcpy(xcc_host, d, (size_t)n_wg * sizeof(int), hipMemcpyDeviceToHost);
     (void)hipFree(d);
-    if (e != hipSuccess) return set_err(h, -EIO, "XCC probe: %s", hipGetErrorString(e));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(h, -EIO, "XCC probe: %s", hipGetErrorString(e));
+    }
     return 0;
 }
 
@@ -577,7 +594,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    h->counter_bytes = (size_t)c.max_batch * c.n_kv_heads * leap::kCounters * sizeof(int);
+    h->counter_bytes = (size_t)c.max_batch * c.n_kv_heads * leap::counters_per_group(h->max_chunks) * sizeof(int);
     CREATE_TRY(hipMalloc(&h->counters, h->counter_bytes));
     CREATE_TRY(hipMemsetAsync(h->counters, 0, h->counter_bytes, h->stream));
     // rounded up to 16 bytes: the inputs are staged in as 16-byte words
@@ -637,6 +654,135 @@ int leap_hip_attention_step_async(leap_hip_attention *h, int layer, int pos, con
                   (hipStream_t)stream);
 }
 
+// ---- the step on caller-owned buffers, allocating nothing ----------------
+//
+// Its split-K workspace (arrival counters, partial (max, sum) records and
+// partial outputs) is this file-scope device array, one copy per device,
+// held until the process ends.  Host code uses the address that
+// hipGetSymbolAddress returns on each device, never the array's name.
+
+}  // extern "C"
+
+namespace {
+
+constexpr size_t kScratchBytes = 4u << 20;
+constexpr int kScratchChunks = 64;  // chunks per launch at most: records_per_head(64) = 72
+constexpr int kScratchDevices = 64;
+constexpr int kScratchMaxKvHeads = 128;
+// The arrival counters sit at the start of the array, in a region of the
+// same size for every shape: the records of one shape must never overlap
+// the counters of another, which have to stay zero between calls.
+constexpr size_t kScratchCounterBytes =
+    (size_t)kScratchMaxKvHeads * leap::counters_per_group(kScratchChunks) * sizeof(int);
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchDevice {
+    std::once_flag once;
+    int rc = 0;
+    unsigned char *ptr = nullptr;  // this device's copy of `scratch`
+    int n_cu = 0;
+    char msg[256] = {};
+};
+ScratchDevice g_scratch[kScratchDevices];
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Bytes of scratch a shape needs: the counter region (fixed), then its
+// (max, sum) records, then its partial outputs, each 256-byte aligned.
+void scratch_layout(const leap_hip_attention_config &c, size_t *ml_off, size_t *o_off, size_t *total)
+{
+    const size_t rec = (size_t)c.n_heads * leap::records_per_head(kScratchChunks);
+    *ml_off = align256(kScratchCounterBytes);
+    *o_off = *ml_off + align256(rec * sizeof(float2));
+    *total = *o_off + rec * (size_t)c.head_dim * sizeof(float);
+}
+
+// Zero n ints on the device (a kernel rather than a memset, so that a
+// caller may capture the first call into a graph).
+__global__ void zero_ints_kernel(int *p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int pos, const float *rope,
+                                    float *k_cache, float *v_cache, const float *q, const float *k_new,
+                                    const float *v_new, float *out, void *stream)
+{
+    if (!cfg) return set_err(nullptr, -EINVAL, "cfg is NULL");
+    const leap_hip_attention_config c = *cfg;
+    if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0)
+        return set_err(nullptr, -EINVAL, "n_heads %d must be a positive multiple of n_kv_heads %d", c.n_heads,
+                       c.n_kv_heads);
+    const int group = c.n_heads / c.n_kv_heads;
+    if (!pick_kernel(c.head_dim, group))
+        return set_err(nullptr, -EINVAL, "unsupported head_dim %d with %d q heads per kv head", c.head_dim, group);
+    if (c.seq_len <= 0) return set_err(nullptr, -EINVAL, "seq_len %d", c.seq_len);
+    if (c.n_kv_heads > kScratchMaxKvHeads)
+        return set_err(nullptr, -EINVAL, "%d kv heads: the static workspace holds counters for %d", c.n_kv_heads,
+                       kScratchMaxKvHeads);
+    const unsigned long long slab_bytes = ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, 1, kWaves)) *
+                                          (unsigned long long)c.n_kv_heads * c.head_dim * sizeof(float);
+    if (slab_bytes >= (1ull << 32))
+        return set_err(nullptr, -EINVAL, "seq_len %d: one layer's cache rows exceed 4 GiB", c.seq_len);
+    if (pos < 0 || pos >= c.seq_len) return set_err(nullptr, -EINVAL, "pos %d outside [0, %d)", pos, c.seq_len);
+    if (!rope || !k_cache || !v_cache || !q || !k_new || !v_new || !out)
+        return set_err(nullptr, -EINVAL, "NULL buffer");
+    if (!aligned16(rope) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(q) || !aligned16(k_new) ||
+        !aligned16(v_new) || !aligned16(out))
+        return set_err(nullptr, -EINVAL, "rope, the caches, q, k_new, v_new and out must be 16-byte aligned");
+    size_t ml_off, o_off, need;
+    scratch_layout(c, &ml_off, &o_off, &need);
+    if (need > kScratchBytes)
+        return set_err(nullptr, -EINVAL,
+                       "%d heads of %d (%d kv heads) need %zu bytes of workspace; the static workspace holds %zu",
+                       c.n_heads, c.head_dim, c.n_kv_heads, need, kScratchBytes);
+    if (c.device < 0 || c.device >= kScratchDevices)
+        return set_err(nullptr, -EINVAL, "device %d outside [0, %d)", c.device, kScratchDevices);
+    if (hipSetDevice(c.device) != hipSuccess) return set_err(nullptr, -ENODEV, "device %d unavailable", c.device);
+    ScratchDevice &d = g_scratch[c.device];
+    std::call_once(d.once, [&]() {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, c.device);
+        if (e == hipSuccess) {
+            // The arrival counters must start at zero (every launch leaves
+            // them at zero, and no shape's records overlap them): the whole
+            // array is cleared once, on the first call's stream, ahead of
+            // its launch.
+            e = launch_k(zero_ints_kernel, dim3(256), dim3(256), (hipStream_t)stream, static_cast<int *>(p),
+                         kScratchBytes / sizeof(int));
+        }
+        if (e != hipSuccess) {
+            d.rc = -EIO;
+            std::snprintf(d.msg, sizeof d.msg, "static workspace on device %d: %s", c.device, hipGetErrorString(e));
+            return;
+        }
+        d.ptr = static_cast<unsigned char *>(p);
+    });
+    if (d.rc) return set_err(nullptr, d.rc, "%s", d.msg);
+    const LaunchShape shape{c.head_dim, group, c.n_heads, c.n_kv_heads, c.seq_len, d.n_cu, 0, kScratchChunks};
+    const LaunchBuffers b{k_cache,
+                          v_cache,
+                          0,
+                          reinterpret_cast<const float4 *>(rope),
+                          reinterpret_cast<float *>(d.ptr + o_off),
+                          reinterpret_cast<float2 *>(d.ptr + ml_off),
+                          reinterpret_cast<int *>(d.ptr)};
+    const hipError_t e = launch_attention(shape, b, 1, nullptr, pos, pos, pos + 1, q, k_new, v_new, out,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(nullptr, -EIO, "launch: %s", hipGetErrorString(e));
+    }
+    return 0;
+}
+
 int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const float *q,
                             const float *k_new, const float *v_new, float *out)
 {
@@ -652,9 +798,8 @@ int leap_hip_attention_step(leap_hip_attention *h, int layer, int pos, const flo
     std::memcpy(h->in_host + qb, k_new, kb);
     std::memcpy(h->in_host + qb + kb, v_new, kb);
     const int n16 = (int)((qb + 2 * kb) / 16);
-    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
-                       reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), s,
+                        reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16));
     const float *qd = reinterpret_cast<const float *>(h->in_dev);
     // The output goes straight to the pinned buffer (device-accessible host
     // memory): the kernel's final stores cross PCIe, with no copy after it.
@@ -718,9 +863,8 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
     std::memcpy(h->in_host + qb + kb, v_new, kb);
     std::memcpy(h->in_host + qb + 2 * kb, pos, n_seq * sizeof(int));
     const int n16 = (int)((qb + 2 * kb + n_seq * sizeof(int) + 15) / 16);  // in_bytes is a multiple of 16
-    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
-                       reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(leap::stage_in_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), s,
+                        reinterpret_cast<float4 *>(h->in_dev), reinterpret_cast<const float4 *>(h->in_host), n16));
     const float *qd = reinterpret_cast<const float *>(h->in_dev);
     const float *kd = qd + (size_t)n_seq * h->q_dim, *vd = kd + (size_t)n_seq * h->kv_dim;
     const int *pd = reinterpret_cast<const int *>(h->in_dev + qb + 2 * kb);
@@ -862,9 +1006,8 @@ int leap_hip_attention_block(leap_hip_attention *h, int layer, int pos, float *x
     float *xd = h->blk + 2 * h->q_dim + 2 * h->kv_dim;
     const size_t xb = (size_t)h->q_dim * sizeof(float);
     std::memcpy(h->out_host, x, xb);  // through pinned memory: staged in by a kernel, one DMA out
-    hipLaunchKernelGGL(leap::stage_in_kernel, dim3((unsigned)((xb / 16 + 255) / 256)), dim3(256), 0, s,
-                       reinterpret_cast<float4 *>(xd), reinterpret_cast<const float4 *>(h->out_host), (int)(xb / 16));
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(leap::stage_in_kernel, dim3((unsigned)((xb / 16 + 255) / 256)), dim3(256), s,
+                        reinterpret_cast<float4 *>(xd), reinterpret_cast<const float4 *>(h->out_host), (int)(xb / 16)));
     if (int rc = launch_block(h, layer, pos, xd, xd, s)) return rc;
     // (adding the wo product straight into the pinned copy measured slower:
     // the residual reads cross PCIe on the wo kernel's critical path)
@@ -993,12 +1136,9 @@ int leap_hip_attention_kv_fill_normal(leap_hip_attention *h, uint64_t seed, floa
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     const size_t n = (size_t)h->cfg.max_batch * h->slab_floats;
     const int blocks = 256 * 16;
-    hipLaunchKernelGGL(leap::fill_normal_kernel, dim3(blocks), dim3(256), 0, h->stream,
-                       h->k_cache, n, seed, scale);
-    HIP_TRY(h, hipGetLastError());
-    hipLaunchKernelGGL(leap::fill_normal_kernel, dim3(blocks), dim3(256), 0, h->stream,
-                       h->v_cache, n, seed ^ 0x5DEECE66DA3B9F21ull, scale);
-    HIP_TRY(h, hipGetLastError());
+    HIP_TRY(h, launch_k(leap::fill_normal_kernel, dim3(blocks), dim3(256), h->stream, h->k_cache, n, seed, scale));
+    HIP_TRY(h, launch_k(leap::fill_normal_kernel, dim3(blocks), dim3(256), h->stream, h->v_cache, n,
+                        seed ^ 0x5DEECE66DA3B9F21ull, scale));
     HIP_TRY(h, hipStreamSynchronize(h->stream));
     return 0;
 }

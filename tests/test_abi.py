@@ -88,3 +88,31 @@ def test_xcc_map_argument_checks():
     assert lib.leap_hip_attention_xcc_map(0, 8, None) == -errno.EINVAL
     if not gpu_available():
         assert lib.leap_hip_attention_xcc_map(0, 8, buf) == -errno.ENODEV
+
+
+def test_step_noalloc_argument_checks():
+    """The allocation-free step rejects bad shapes and arguments before it
+    touches a device (through the Python binding, so its signature is
+    exercised too)."""
+    with pytest.raises(A.LeapError) as ei:
+        A.step_noalloc(8, 3, 128, 64, 0, 16, 16, 16, 16, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "multiple" in str(ei.value)
+    with pytest.raises(A.LeapError) as ei:
+        A.step_noalloc(8, 2, 96, 64, 0, 16, 16, 16, 16, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "head_dim" in str(ei.value)
+    with pytest.raises(A.LeapError) as ei:
+        A.step_noalloc(8, 2, 128, 64, 64, 16, 16, 16, 16, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "pos" in str(ei.value)
+    with pytest.raises(A.LeapError) as ei:
+        A.step_noalloc(8, 2, 128, 64, 0, 16, 16, 16, 0, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "NULL" in str(ei.value)
+    with pytest.raises(A.LeapError) as ei:
+        A.step_noalloc(8, 2, 128, 64, 0, 20, 16, 16, 16, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "aligned" in str(ei.value)
+    with pytest.raises(A.LeapError) as ei:  # 128 heads of 128: 4.7 MB of records
+        A.step_noalloc(128, 16, 128, 64, 0, 16, 16, 16, 16, 16, 16, 16)
+    assert ei.value.code == -errno.EINVAL and "workspace" in str(ei.value)
+    if not gpu_available():
+        with pytest.raises(A.LeapError) as ei:
+            A.step_noalloc(8, 2, 128, 64, 0, 16, 16, 16, 16, 16, 16, 16)
+        assert ei.value.code == -errno.ENODEV
