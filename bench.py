@@ -13,15 +13,32 @@ timed region, with B(T) = 8*T*kv_dim + 8*dim + 16*kv_dim + 4*head_dim bytes
 per layer-step and sequence; microseconds per layer-step and the fraction of
 the 8 TB/s HBM peak alongside.
 
-The CPU baseline is the reference's own code (oracle/_ref, built from its
-sources with its release flags) timed on the host cores on a bounded sample of
-the same workload, with sequence 0's device cache bytes downloaded.  The
-reference keeps its attention inline in run_layer, between the projections:
-for the attention workloads, calls at the workload's position and at position
-0 alternate, and the difference of their medians is the attention; for the
-sub-block workloads, run_layer itself is timed (zero FFN).  Without that
-library (or for a RoPE base other than the reference's fixed 500000), the
-oracle, the restated reference (OpenMP over heads, AVX2), is timed instead.
+The default run's line also carries, for the same build and box:
+  - `floor`: the same launch shape (grid, block, argument block) running a
+    kernel that only reads its arguments, and one that only streams the same
+    K/V rows with the same loads; the per-launch cost any one-launch design
+    pays at this shape;
+  - `workloads`: the other configurations, each allocated, filled, timed
+    (events over >= 10 steps) and freed in turn: TinyLlama ctx 256, a batch
+    of 64 Llama-3-8B sequences with ragged contexts in [512, 8192], a
+    Llama-3-70B pipeline stage (20 layers, batch 16, ctx 8192) and
+    Llama-3.1-8B at ctx 131072;
+  - `t_sweep`: microseconds per layer-step over contexts 1 .. 4096 at the
+    Llama-3-8B and TinyLlama head shapes, eager and replayed from a HIP graph
+    (every decode walks these contexts from position 0);
+  - `cpu_baseline`: the reference's own code (oracle/_ref, built from its
+    sources with its release flags) on the host cores, in a child process
+    pinned as the reference's README says (OMP_PROC_BIND=close,
+    OMP_PLACES=cores), at min(n_heads, physical cores) threads and at every
+    usable logical CPU, on a bounded sample of the same workload with
+    sequence 0's device cache bytes downloaded.  The reference keeps its
+    attention inline in run_layer, between the projections: for the
+    attention workloads, calls at the workload's position and at position 0
+    alternate, and the difference of their medians is the attention; for the
+    sub-block workloads, run_layer itself is timed (zero FFN).  Without that
+    library (or for a RoPE base other than the reference's fixed 500000), the
+    oracle, the restated reference (OpenMP over heads, AVX2), is timed
+    instead.
 
 The `*-block-*` workloads time the whole attention sub-block of the layer step
 instead (rmsnorm, q/k/v projections, attention, wo projection and residual;
@@ -40,6 +57,7 @@ inputs and result over PCIe and waits for them in every call.  It is reported
 beside `value`, never as `value`.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
+                    [--no-extra] [--no-host-pointer] [--no-graph]
 """
 from __future__ import annotations
 
@@ -47,7 +65,9 @@ import argparse
 import json
 import os
 import re
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -55,13 +75,10 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-METRIC = "attn decode µs/layer-step + HBM GB/s (% of peak), Llama-3-8B shape ctx 4096"
+HEADLINE_METRIC = "attn decode µs/layer-step + HBM GB/s (% of peak), Llama-3-8B shape ctx 4096"
 HBM_PEAK_GBS = 8000.0
 KERNEL = "decode_attention_kernel"
-BLOCK_METRIC = "attn sub-block (rmsnorm, qkv, attention, wo, residual) µs/layer-step + HBM GB/s, Llama-3-8B ctx 4096"
 BLOCK_KERNELS = "qkv_kernel + decode_attention_kernel + proj_residual_kernel"
-Q8_METRIC = ("attn sub-block, int8 weights (rmsnorm, quantize, W8A8 qkv, attention, quantize, W8A8 wo, residual) "
-             "µs/layer-step + HBM GB/s, Llama-3-8B ctx 4096")
 Q8_KERNELS = "q8_gemv_kernel (qkv) + decode_attention_kernel + q8_gemv_kernel (wo)"
 Q8_GROUP = 64
 SEED = 0x4C454150
@@ -78,12 +95,39 @@ WORKLOADS = {
     "llama3-8b-q8-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 6),
     "llama3.2-3b-ctx4096": (28, 24, 8, 128, 500000.0, 1, 4096, 7),
 }
+SHAPE_NAMES = {
+    "llama3-8b-ctx4096": "Llama-3-8B shape ctx 4096",
+    "tinyllama-ctx256": "TinyLlama-1.1B shape (32/4/64) ctx 256, one layer",
+    "llama3-8b-batch64-ragged": "Llama-3-8B shape, 64 sequences, ctx U[512, 8192]",
+    "llama3-70b-stage20-batch16": "Llama-3-70B stage (64/8/128, 20 layers), 16 sequences, ctx 8192",
+    "llama3.1-8b-ctx131072": "Llama-3.1-8B shape ctx 131072",
+    "llama3-8b-block-ctx4096": "Llama-3-8B ctx 4096",
+    "llama3-8b-q8-block-ctx4096": "Llama-3-8B ctx 4096",
+    "llama3.2-3b-ctx4096": "Llama-3.2-3B shape (24/8/128) ctx 4096",
+}
 BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096", "llama3-8b-q8-block-ctx4096"}
 Q8_WORKLOADS = {"llama3-8b-q8-block-ctx4096"}
 DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3-8b-batch64-ragged": 10, "llama3-70b-stage20-batch16": 10,
                  "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30,
                  "llama3-8b-q8-block-ctx4096": 50, "llama3.2-3b-ctx4096": 100}
+# the configurations timed beside the headline in the default run
+EXTRA_WORKLOADS = ("tinyllama-ctx256", "llama3-8b-batch64-ragged", "llama3-70b-stage20-batch16",
+                   "llama3.1-8b-ctx131072")
+SWEEP_T = (1, 16, 64, 256, 1024, 2048, 4096)
+SWEEP_SHAPES = {"llama3-8b": (32, 32, 8, 128, 500000.0), "tinyllama": (22, 32, 4, 64, 10000.0)}
+
+
+def metric_for(workload: str) -> str:
+    if workload == "llama3-8b-ctx4096":
+        return HEADLINE_METRIC
+    if workload in Q8_WORKLOADS:
+        return ("attn sub-block, int8 weights (rmsnorm, quantize, W8A8 qkv, attention, quantize, W8A8 wo, "
+                f"residual) µs/layer-step + HBM GB/s, {SHAPE_NAMES[workload]}")
+    if workload in BLOCK_WORKLOADS:
+        return (f"attn sub-block (rmsnorm, qkv, attention, wo, residual) µs/layer-step + HBM GB/s, "
+                f"{SHAPE_NAMES[workload]}")
+    return f"attn decode µs/layer-step + HBM GB/s (% of peak), {SHAPE_NAMES[workload]}"
 
 
 def algorithmic_bytes(T: int, n_heads: int, n_kv: int, hd: int) -> int:
@@ -121,27 +165,12 @@ def quantize_groups(w: np.ndarray, gs: int):
     return q.reshape(w.shape), sc
 
 
-def hip_graph_us(one_step, stream, steps: int, n_layers: int) -> float:
-    """Microseconds per layer-step of one_step captured once into a HIP graph
-    (its launches only: the entry points enqueue kernels and nothing else)
-    and replayed `steps` times on `stream`."""
-    import torch
-    graph = torch.cuda.CUDAGraph()
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph, stream=stream):
-        one_step()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        for _ in range(2):
-            graph.replay()
-        e0.record(stream)
-        for _ in range(steps):
-            graph.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / (steps * n_layers)
+def contexts(workload: str):
+    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    if isinstance(ctx, tuple):
+        rng = np.random.default_rng(SEED + sidx)
+        return rng.integers(ctx[1], ctx[2] + 1, size=batch).astype(np.int64)
+    return np.full(batch, ctx, np.int64)
 
 
 def traffic_from_profiles(workload: str):
@@ -154,171 +183,427 @@ def traffic_from_profiles(workload: str):
     return float(m.group(1)) if m else None
 
 
-def contexts(workload: str):
-    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
-    if isinstance(ctx, tuple):
-        rng = np.random.default_rng(SEED + sidx)
-        return rng.integers(ctx[1], ctx[2] + 1, size=batch).astype(np.int64)
-    return np.full(batch, ctx, np.int64)
+# ---- timing helpers -------------------------------------------------------------
+
+def timed_steps(one_step, stream, steps: int, warmup: int, n_layers: int):
+    """Run `warmup` untimed steps, then exactly `steps` steps bracketed by a
+    device synchronisation on both sides, cut into up to 10 segments by
+    events on `stream`.  Returns (total ms, per-segment us per layer-step,
+    host wall seconds)."""
+    import torch
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    n_seg = min(10, steps)
+    bounds = [round(i * steps / n_seg) for i in range(n_seg + 1)]
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_seg + 1)]
+    torch.cuda.synchronize()
+    evs[0].record(stream)
+    t0 = time.perf_counter()
+    for i in range(n_seg):
+        for _ in range(bounds[i + 1] - bounds[i]):
+            one_step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = evs[0].elapsed_time(evs[-1])
+    seg_us = np.array([evs[i].elapsed_time(evs[i + 1]) * 1e3 / ((bounds[i + 1] - bounds[i]) * n_layers)
+                       for i in range(n_seg)])
+    return ms_total, seg_us, wall
 
 
-def cpu_baseline_block(att, workload, Ts, n_layers_sample: int, budget_s: float, weights, q8: bool = False):
-    """The sub-block on the host cores, on the device cache bytes of layer 0
-    (downloaded).  When oracle/_ref is present: the reference's own run_layer
-    (compiled from its sources with its release flags, OpenMP as it ships) on
-    an engine whose layers each hold these weights and a zero FFN of
-    negligible size, cycled so that the weights come from memory.  Otherwise:
-    the oracle's chain (rmsnorm, matmul, attention, matmul, residual) on layers
-    [0, n_layers_sample)."""
-    from oracle import oracle as O
-    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
-    T = int(Ts[0])
-    x0 = np.random.default_rng(SEED + sidx).standard_normal(nh * hd).astype(np.float32)
-    nbytes = (q8_block_bytes if q8 else block_bytes)(T, nh, nkv, hd)
-    if (O.ref_q8_available() if q8 else O.ref_available()) and theta == 500000.0:
-        k, v = att.kv_download(0, 0, 0, T - 1)
-        # enough layers (each its own copy of the weights and cache rows) that
-        # the CPU caches cannot hold them: about 1.6 GB
-        n_l = max(4, -(-1_600_000_000 // nbytes))
-        timer = O.RefBlockTimer(nh * hd, nh, nkv, T, *weights, k, v, gs=Q8_GROUP if q8 else None, n_layers=n_l)
+def hip_graph_us(one_step, stream, steps: int, n_layers: int) -> float:
+    """Microseconds per layer-step of one_step captured into a HIP graph (its
+    launches only: the entry points enqueue kernels and nothing else) and
+    replayed on `stream`.  A graph holds enough steps for at least 32
+    launches (replaying a graph has a fixed cost of its own), and is
+    replayed until at least `steps` steps have run."""
+    import torch
+    per_graph = max(1, -(-32 // n_layers))
+    replays = max(2, -(-steps // per_graph))
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(per_graph):
+            one_step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            graph.replay()
+        e0.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * per_graph * n_layers)
+    del graph
+    return us
+
+
+class Workload:
+    """One configuration on the device: the handle, its filled cache, the
+    step's inputs, and one_step() running the layer sweep on `stream`."""
+
+    def __init__(self, workload: str, split: int = 0):
+        import torch
+        from leap_amd.attention import HipAttention
+        self.name = workload
+        L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+        self.L, self.nh, self.nkv, self.hd, self.theta, self.batch, self.sidx = L, nh, nkv, hd, theta, batch, sidx
+        self.Ts = contexts(workload)
+        self.is_block = workload in BLOCK_WORKLOADS
+        self.is_q8 = workload in Q8_WORKLOADS
+        dev = torch.device("cuda:0")
+        self.att = att = HipAttention(nh, nkv, hd, int(self.Ts.max()), n_layers=L, rope_theta=theta,
+                                      max_batch=batch)
+        if split:
+            att.set_split(split)
+        att.kv_fill_normal(SEED + sidx, 1.0 / np.sqrt(hd))
+        g = torch.Generator(device=dev)
+        g.manual_seed(SEED + sidx)
+        scale = 1.0 / np.sqrt(hd)
+        self.q = torch.randn(L, batch, nh * hd, device=dev, generator=g) * scale
+        self.k = torch.randn(L, batch, nkv * hd, device=dev, generator=g) * scale
+        self.v = torch.randn(L, batch, nkv * hd, device=dev, generator=g) * scale
+        self.out = torch.empty(L, batch, nh * hd, device=dev)
+        self.pos_dev = torch.tensor(self.Ts - 1, dtype=torch.int32, device=dev)
+        self.max_pos = int(self.Ts.max()) - 1
+        self.total_rows = int(np.sum(self.Ts))
+        self.stream = torch.cuda.Stream(device=dev)
+        sp = self.stream.cuda_stream
+        ptrs = [(self.q[l].data_ptr(), self.k[l].data_ptr(), self.v[l].data_ptr(), self.out[l].data_ptr())
+                for l in range(L)]
+        self.weights = None
+        if self.is_block:
+            dim, kvd = nh * hd, nkv * hd
+            wrng = np.random.default_rng(SEED + sidx)
+            w = (
+                (1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32),
+                (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
+                (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
+                (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
+                (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
+            )
+            if self.is_q8:
+                w = (w[0],) + tuple(quantize_groups(x, Q8_GROUP) for x in w[1:])
+                for l in range(L):
+                    att.set_layer_weights_q8(l, Q8_GROUP, *w)
+            else:
+                for l in range(L):
+                    att.set_layer_weights(l, *w)
+            self.weights = w
+            self.x_res = torch.randn(dim, device=dev, generator=g)
+            xp = self.x_res.data_ptr()
+            pos = int(self.Ts[0]) - 1
+
+            def one_step():
+                for l in range(L):
+                    att.block_async(l, pos, xp, sp)
+        elif batch == 1:
+            pos = int(self.Ts[0]) - 1
+
+            def one_step():
+                for l in range(L):
+                    qp, kp, vp, op = ptrs[l]
+                    att.step_async(l, pos, qp, kp, vp, op, sp)
+        else:
+            pp = self.pos_dev.data_ptr()
+            max_pos, total_rows = self.max_pos, self.total_rows
+
+            def one_step():
+                for l in range(L):
+                    qp, kp, vp, op = ptrs[l]
+                    att.step_batched_async(l, batch, pp, max_pos, qp, kp, vp, op, sp, total_rows)
+        self.one_step = one_step
+        per_seq = q8_block_bytes if self.is_q8 else block_bytes if self.is_block else algorithmic_bytes
+        self.bytes_layer = int(sum(per_seq(int(T), nh, nkv, hd) for T in self.Ts))
+
+    def finite(self) -> bool:
+        return bool(np.isfinite((self.x_res if self.is_block else self.out).float().sum().item()))
+
+    def floor_us(self, kind: int, steps: int, warmup: int) -> float:
+        """Microseconds per layer-step of the floor launches (kind 1: the
+        launch alone, kind 2: the bare K/V stream) with this step's shape."""
+        att, sp, L = self.att, self.stream.cuda_stream, self.L
+        n, mp, tr = self.batch, self.max_pos, (self.total_rows if self.batch > 1 else self.max_pos + 1)
+
+        def one():
+            for l in range(L):
+                att.floor_async(kind, l, n, mp, tr, sp)
+        ms, _, _ = timed_steps(one, self.stream, steps, warmup, L)
+        return ms * 1e3 / (steps * L)
+
+    def close(self):
+        self.att.close()
+        for name in ("q", "k", "v", "out", "pos_dev", "x_res"):
+            if hasattr(self, name):
+                delattr(self, name)
+
+
+def measure(w: Workload, steps: int, warmup: int, graph: bool = True):
+    ms_total, seg_us, wall = timed_steps(w.one_step, w.stream, steps, warmup, w.L)
+    us_layer = ms_total * 1e3 / (steps * w.L)
+    r = {
+        "us_per_layer_step": round(us_layer, 3),
+        "value": round(w.bytes_layer / (us_layer * 1e-6) / 1e9, 2),
+        "unit": "GB/s",
+        "frac": round(w.bytes_layer / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_launch": w.bytes_layer,
+        "steps": steps, "warmup": warmup, "ms_total": ms_total, "wall": wall,
+        "spread": {"segments": len(seg_us), "median": round(float(np.median(seg_us)), 3),
+                   "p10": round(float(np.percentile(seg_us, 10)), 3),
+                   "p90": round(float(np.percentile(seg_us, 90)), 3)},
+    }
+    if graph:
+        gus = hip_graph_us(w.one_step, w.stream, steps, w.L)
+        r["hip_graph_us"] = round(gus, 3)
+    return r
+
+
+def extra_workload(name: str):
+    """One of the other configurations: allocated, filled, timed and freed."""
+    import torch
+    steps = max(10, min(DEFAULT_STEPS[name], 200))
+    w = Workload(name)
+    try:
+        r = measure(w, steps, 3)
+        ok = w.finite()
+    finally:
+        w.close()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[name]
+    Ts = contexts(name)
+    return {
+        "metric": metric_for(name), "us_per_layer_step": r["us_per_layer_step"], "value": r["value"],
+        "unit": "GB/s", "frac": r["frac"], "hip_graph_us_per_layer_step": r["hip_graph_us"],
+        "bytes_per_launch": r["bytes_per_launch"], "steps": steps,
+        "tokens_layers_per_s": round(batch * 1e6 / r["us_per_layer_step"], 1),
+        "config": {"n_layers": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "batch": batch,
+                   "rope_theta": theta,
+                   "context": int(Ts[0]) if batch == 1 else {"min": int(Ts.min()), "max": int(Ts.max()),
+                                                             "sum": int(Ts.sum())}},
+        "finite": ok,
+    }
+
+
+def t_sweep():
+    """Microseconds per layer-step over short to long contexts (eager launches
+    and HIP graph replay) at two head shapes; each layer its own cache rows."""
+    import torch
+    from leap_amd.attention import HipAttention
+    dev = torch.device("cuda:0")
+    res = {}
+    for name, (L, nh, nkv, hd, th) in SWEEP_SHAPES.items():
+        att = HipAttention(nh, nkv, hd, max(SWEEP_T), n_layers=L, rope_theta=th)
         try:
-            x = x0.copy()
-            timer.run(T - 1, x, 1)  # the OpenMP pool starts
-            times = []
-            t_end = time.perf_counter() + budget_s
-            while time.perf_counter() < t_end or len(times) < 3:
+            att.kv_fill_normal(SEED + 11, 1 / np.sqrt(hd))
+            q = torch.randn(L, nh * hd, device=dev) / np.sqrt(hd)
+            k = torch.randn(L, nkv * hd, device=dev) / np.sqrt(hd)
+            v = torch.randn(L, nkv * hd, device=dev) / np.sqrt(hd)
+            out = torch.empty(L, nh * hd, device=dev)
+            s = torch.cuda.Stream()
+            sp = s.cuda_stream
+            ptrs = [(q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(), out[l].data_ptr()) for l in range(L)]
+            rows = {}
+            for T in SWEEP_T:
+                def one_step():
+                    for l in range(L):
+                        att.step_async(l, T - 1, *ptrs[l], sp)
+                ms, _, _ = timed_steps(one_step, s, 100, 10, L)
+                eager = ms * 1e3 / (100 * L)
+                gus = hip_graph_us(one_step, s, 100, L)
+                rows[str(T)] = {"eager_us": round(eager, 3), "graph_us": round(gus, 3),
+                                "graph_GBps": round(algorithmic_bytes(T, nh, nkv, hd) / (gus * 1e-6) / 1e9, 1)}
+            res[name] = {"n_layers": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "T": rows}
+        finally:
+            att.close()
+    res["note"] = ("eager: one Python ctypes call per launch, which costs about 7 us of host time, so short "
+                   "contexts are host-bound there; graph: the same launches replayed from a HIP graph")
+    return res
+
+
+# ---- CPU baseline (the reference's own code, or the oracle) ------------------------
+
+def host_cpu():
+    """CPU model, usable logical CPUs, physical cores among them, AVX-512F."""
+    model, flags = "unknown", ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = line.split(":", 1)[1]
+    except OSError:
+        pass
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        try:
+            core = open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read().strip()
+            pkg = open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    return {"model": model, "logical_cpus": len(cpus), "physical_cores": len(cores),
+            "avx512f": " avx512f " in f" {flags} "}
+
+
+def cpu_leg_child(spec_path: str):
+    """The CPU leg proper, in a child process whose OpenMP settings the parent
+    fixed (no GPU, no torch): prints one JSON object."""
+    from oracle import oracle as O
+    spec = json.load(open(spec_path))
+    data = np.load(spec["data"])
+    T, budget, kind = spec["T"], spec["budget_s"], spec["kind"]
+    dim, nh, nkv = spec["dim"], spec["n_heads"], spec["n_kv"]
+    if kind in ("attention", "block", "block_q8"):
+        if kind == "attention":
+            w = [data["rms"], data["wq"], data["wk"], data["wv"], data["wo"]]
+            gs = None
+        elif kind == "block":
+            w = [data["rms"], data["wq"], data["wk"], data["wv"], data["wo"]]
+            gs = None
+        else:
+            w = [data["rms"]] + [(data[f"{n}_q"], data[f"{n}_s"]) for n in ("wq", "wk", "wv", "wo")]
+            gs = Q8_GROUP
+        timer = O.RefBlockTimer(dim, nh, nkv, T, *w, data["k"], data["v"], gs=gs, n_layers=spec["n_layers"])
+        x0 = data["x"]
+        x = x0.copy()
+        long_t, short_t = [], []
+        try:
+            timer.run(T - 1, x, spec["n_layers"])  # the OpenMP pool starts, every layer touched once
+            t_end = time.perf_counter() + budget
+            while time.perf_counter() < t_end or len(long_t) < 5:
                 x[:] = x0
-                times.append(timer.run(T - 1, x, 1))
+                long_t.append(timer.run(T - 1, x, 1))
+                if kind == "attention":
+                    x[:] = x0
+                    short_t.append(timer.run(0, x, 1))
         finally:
             timer.close()
-        us = float(np.median(times)) * 1e6
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
-        return {
-            "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
-            "us_per_layer_step": round(us, 2),
-            "sample": f"{len(times)} calls of the reference's {'QuantizedTransformer' if q8 else 'FloatTransformer'}"
-                      f"::run_layer at pos {T - 1}, cycling through an engine of {n_l} layers that each hold "
-                      f"the workload's weights (zero FFN of hidden size {Q8_GROUP if q8 else 8}) and layer 0's "
-                      f"device cache rows; median per call; the reference's own OpenMP",
-        }
-    if not os.path.isfile(O.ORACLE_SO):
-        O.build(ref=False)
-    env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    threads = min(env_threads or os.cpu_count() or 1, 16)
-    O.lib().oracle_set_threads(threads)
-    n_l = min(n_layers_sample, L)
-    orc = O.Oracle(n_l, nh, nkv, hd, T, theta=theta)
-    for l in range(n_l):
-        k, v = att.kv_download(0, l, 0, T)
-        orc.key_cache[l] = k
-        orc.value_cache[l] = v
-    x = x0
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
+        us = float(np.median(long_t)) * 1e6
+        res = {"calls": len(long_t), "long_us": us}
+        if kind == "attention":
+            res["short_us"] = float(np.median(short_t)) * 1e6
+            us -= res["short_us"]
+        res["us"] = us
+    else:  # the oracle restatement of the attention step
+        O.lib().oracle_set_threads(spec["threads"])
+        n_l = data["k"].shape[0]
+        hd = dim // nh
+        orc = O.Oracle(n_l, nh, nkv, hd, T, theta=spec["theta"])
         for l in range(n_l):
-            if q8:
-                orc.block_q8(l, T - 1, x, *weights, Q8_GROUP)
-            else:
-                orc.block(l, T - 1, x, *weights)
-        times.append((time.perf_counter() - t0) / n_l)
-    us = float(np.median(times)) * 1e6
-    return {
-        "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "us_per_layer_step": round(us, 2),
-        "sample": f"{len(times)} sweeps of the sub-block over layers 0..{n_l - 1} of the same workload "
-                  f"(context {T}), device cache bytes downloaded; median per layer-step; OpenMP over "
-                  f"rows and heads",
-    }
+            orc.key_cache[l, :T - 1] = data["k"][l]
+            orc.value_cache[l, :T - 1] = data["v"][l]
+        rng = np.random.default_rng(SEED)
+        qs = [(rng.standard_normal(dim) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
+        ks = [(rng.standard_normal(nkv * hd) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
+        vs = [(rng.standard_normal(nkv * hd) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
+        times = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            for l in range(n_l):
+                orc.step(l, T - 1, qs[l], ks[l], vs[l])
+            times.append((time.perf_counter() - t0) / n_l)
+        res = {"calls": len(times), "us": float(np.median(times)) * 1e6}
+    print(json.dumps(res), flush=True)
 
 
-def cpu_baseline_reference(att, workload, T: int, budget_s: float):
-    """The reference's own attention on the host cores, timed through its
-    run_layer (oracle/_ref), which holds the attention inline between the
-    projections: calls at pos T-1 and at pos 0 alternate on an engine of
-    several layers (each its own copy of synthetic weights and of sequence
-    0's first T-1 device cache rows, cycled so that nothing stays in the CPU
-    caches), and the difference of their medians is the attention over T
-    rows; the projections, the residual and the zero FFN are the same work
-    in both."""
+def cpu_baseline(w: Workload, budget_s: float, cpu_layers: int):
+    """The CPU baseline of workload `w` on the host cores at min(n_heads,
+    physical cores) threads and at every usable logical CPU, each in a child
+    process with OMP_PROC_BIND=close OMP_PLACES=cores (the reference README's
+    pinning).  The data (sequence 0's first T-1 device cache rows, synthetic
+    weights) is written to a temporary file the child reads."""
     from oracle import oracle as O
-    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
+    cpu = host_cpu()
+    T = int(w.Ts[0])
+    nh, nkv, hd = w.nh, w.nkv, w.hd
     dim, kvd = nh * hd, nkv * hd
-    wrng = np.random.default_rng(SEED + sidx)
-    w = [(1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32)] + [
-        (wrng.standard_normal(shape) / np.sqrt(dim)).astype(np.float32)
-        for shape in ((dim, dim), (kvd, dim), (kvd, dim), (dim, dim))]
-    k, v = att.kv_download(0, 0, 0, T - 1)
-    per_layer = 4 * (2 * dim * dim + 2 * kvd * dim) + 8 * T * kvd
-    n_l = max(4, -(-1_600_000_000 // per_layer))
-    timer = O.RefBlockTimer(dim, nh, nkv, T, *w, k, v, n_layers=n_l)
-    x0 = wrng.standard_normal(dim).astype(np.float32)
-    x = x0.copy()
-    long_t, short_t = [], []
-    try:
-        timer.run(T - 1, x, n_l)  # the OpenMP pool starts, every layer touched once
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end or len(long_t) < 5:
-            x[:] = x0
-            long_t.append(timer.run(T - 1, x, 1))
-            x[:] = x0
-            short_t.append(timer.run(0, x, 1))
-    finally:
-        timer.close()
-    us = (float(np.median(long_t)) - float(np.median(short_t))) * 1e6
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count() or 1
+    variant = "v4" if cpu["avx512f"] else "v3"
+    env_base = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores", LEAP_REF_VARIANT=variant)
+    ref_ok = (O.ref_q8_available() if w.is_q8 else O.ref_available()) and w.theta == 500000.0
+    if ref_ok:
+        kind = "block_q8" if w.is_q8 else "block" if w.is_block else "attention"
+        if w.is_block:
+            nbytes = w.bytes_layer
+            arrays = {"rms": w.weights[0]}
+            if w.is_q8:
+                for n, (q, sc) in zip(("wq", "wk", "wv", "wo"), w.weights[1:]):
+                    arrays[f"{n}_q"], arrays[f"{n}_s"] = q, sc
+            else:
+                arrays.update(zip(("wq", "wk", "wv", "wo"), w.weights[1:]))
+            per_layer = nbytes
+        else:
+            nbytes = algorithmic_bytes(T, nh, nkv, hd)
+            wrng = np.random.default_rng(SEED + w.sidx)
+            arrays = {"rms": (1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32)}
+            for n, shape in (("wq", (dim, dim)), ("wk", (kvd, dim)), ("wv", (kvd, dim)), ("wo", (dim, dim))):
+                arrays[n] = (wrng.standard_normal(shape) / np.sqrt(dim)).astype(np.float32)
+            per_layer = 4 * (2 * dim * dim + 2 * kvd * dim) + 8 * T * kvd
+        arrays["k"], arrays["v"] = w.att.kv_download(0, 0, 0, T - 1)
+        arrays["x"] = np.random.default_rng(SEED + w.sidx + 100).standard_normal(dim).astype(np.float32)
+        # enough layers (each its own copy of the weights and cache rows) that the
+        # host's caches cannot hold them: about 1.6 GB
+        n_layers = max(4, -(-1_600_000_000 // per_layer))
+    else:
+        kind = "oracle"
+        nbytes = algorithmic_bytes(T, nh, nkv, hd)
+        n_layers = min(cpu_layers, w.L)
+        ks, vs = zip(*[w.att.kv_download(0, l, 0, T - 1) for l in range(n_layers)])
+        arrays = {"k": np.stack(ks), "v": np.stack(vs)}
+        if not os.path.isfile(O.ORACLE_SO):
+            O.build(ref=False)
+    counts = sorted({min(nh, cpu["physical_cores"]), cpu["logical_cpus"]})
+    runs = {}
+    with tempfile.TemporaryDirectory(prefix="leap_cpu_leg_") as tmp:
+        data_path = os.path.join(tmp, "data.npz")
+        np.savez(data_path, **arrays)
+        for threads in counts:
+            spec = {"data": data_path, "T": T, "budget_s": budget_s / len(counts), "kind": kind, "dim": dim,
+                    "n_heads": nh, "n_kv": nkv, "n_layers": n_layers, "threads": threads, "theta": w.theta}
+            spec_path = os.path.join(tmp, f"spec{threads}.json")
+            json.dump(spec, open(spec_path, "w"))
+            env = dict(env_base, OMP_NUM_THREADS=str(threads))
+            r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg", spec_path], env=env,
+                               capture_output=True, text=True, timeout=budget_s * 4 + 120)
+            if r.returncode != 0:
+                raise RuntimeError(f"CPU leg with {threads} threads failed: {r.stderr[-400:]}")
+            runs[threads] = json.loads(r.stdout.strip().splitlines()[-1])
+    best_t = min(runs, key=lambda t: runs[t]["us"])
+    us = runs[best_t]["us"]
+    lib_name = ("QuantizedTransformer" if w.is_q8 else "FloatTransformer")
+    if kind == "attention":
+        r0 = runs[best_t]
+        sample = (f"the reference's FloatTransformer::run_layer, {r0['calls']} calls each at pos {T - 1} and pos 0 "
+                  f"alternating over an engine of {n_layers} layers (synthetic weights, sequence 0's device cache "
+                  f"rows); attention = difference of the medians ({r0['long_us']:.1f} - {r0['short_us']:.1f} us)")
+    elif kind in ("block", "block_q8"):
+        sample = (f"{runs[best_t]['calls']} calls of the reference's {lib_name}::run_layer at pos {T - 1}, cycling "
+                  f"through an engine of {n_layers} layers that each hold the workload's weights (zero FFN) and "
+                  f"layer 0's device cache rows; median per call")
+    else:
+        sample = (f"{runs[best_t]['calls']} sweeps of the oracle (the restated reference, OpenMP over heads, AVX2) "
+                  f"over layers 0..{n_layers - 1} of sequence 0 (context {T}), device cache bytes downloaded; "
+                  f"median per layer-step")
     return {
-        "value": round(algorithmic_bytes(T, nh, nkv, hd) / (us * 1e-6) / 1e9, 3), "unit": "GB/s",
-        "cores": threads, "kind": "reference", "us_per_layer_step": round(us, 2),
-        "sample": f"the reference's FloatTransformer::run_layer, {len(long_t)} calls each at pos {T - 1} and pos 0 "
-                  f"alternating over an engine of {n_l} layers (synthetic weights, sequence 0's device cache "
-                  f"rows); attention = difference of the medians ({float(np.median(long_t)) * 1e6:.1f} - "
-                  f"{float(np.median(short_t)) * 1e6:.1f} us); the reference's own OpenMP",
-    }
-
-
-def cpu_baseline(att, workload, Ts, n_layers_sample: int, budget_s: float):
-    """The reference's attention through its run_layer when oracle/_ref is
-    present and the workload uses the reference's fixed RoPE base; otherwise
-    the oracle on the host on layers [0, n_layers_sample) of sequence 0 of
-    the device cache (downloaded bytes), repeating sweeps for about budget_s
-    seconds."""
-    from oracle import oracle as O
-    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[workload]
-    if O.ref_available() and theta == 500000.0:
-        return cpu_baseline_reference(att, workload, int(Ts[0]), budget_s)
-    if not os.path.isfile(O.ORACLE_SO):
-        O.build(ref=False)
-    env_threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    threads = min(nh, env_threads or os.cpu_count() or 1, 16)
-    O.lib().oracle_set_threads(threads)
-    T = int(Ts[0])
-    n_l = min(n_layers_sample, L)
-    rng = np.random.default_rng(SEED + sidx)
-    orc = O.Oracle(n_l, nh, nkv, hd, T, theta=theta)
-    for l in range(n_l):
-        k, v = att.kv_download(0, l, 0, T)
-        orc.key_cache[l] = k
-        orc.value_cache[l] = v
-    qs = [(rng.standard_normal(nh * hd) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
-    ks = [(rng.standard_normal(nkv * hd) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
-    vs = [(rng.standard_normal(nkv * hd) / np.sqrt(hd)).astype(np.float32) for _ in range(n_l)]
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        for l in range(n_l):
-            orc.step(l, T - 1, qs[l], ks[l], vs[l])
-        times.append((time.perf_counter() - t0) / n_l)
-    us = float(np.median(times)) * 1e6
-    gbs = algorithmic_bytes(T, nh, nkv, hd) / (us * 1e-6) / 1e9
-    return {
-        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "us_per_layer_step": round(us, 2),
-        "sample": f"{len(times)} sweeps of layers 0..{n_l - 1} of sequence 0 (context {T}) of the "
-                  f"same workload, device cache bytes downloaded; median per layer-step; "
-                  f"OpenMP over heads",
+        "value": round(nbytes / (us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": best_t,
+        "kind": "reference" if ref_ok else "port", "us_per_layer_step": round(us, 2),
+        "by_threads": {str(t): {"us_per_layer_step": round(r["us"], 2),
+                                "value": round(nbytes / (r["us"] * 1e-6) / 1e9, 3)} for t, r in runs.items()},
+        "threads_note": f"min(n_heads, physical cores) = {min(nh, cpu['physical_cores'])}, "
+                        f"all usable logical CPUs = {cpu['logical_cpus']}; `value` is the faster",
+        "cpu": cpu, "omp": "OMP_PROC_BIND=close OMP_PLACES=cores (the reference README's pinning)",
+        "march": (f"x86-64-{variant} with the reference's other release flags (-O3 -ffast-math -funroll-loops "
+                  f"-fomit-frame-pointer -fopenmp); its CMakeLists.txt:33 says -march=native, which needs the "
+                  f"sources on the host that runs it; the reference has only NEON and AVX2 paths, so both take "
+                  f"its __AVX2__ code"),
+        "sample": sample,
     }
 
 
@@ -377,14 +662,20 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-host-pointer", action="store_true",
                     help="skip the host-pointer (PCIe-inclusive) leg, e.g. under a profiler")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the floor, the other workloads and the context sweep")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--split", type=int, default=0, help="positions per split-K chunk (0 = auto)")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay timing")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--cpu-leg", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_leg:
+        cpu_leg_child(args.cpu_leg)
+        return
     if args.copy_probe:
         import torch
         n = args.copy_probe * (1 << 20) // 4
@@ -405,124 +696,33 @@ def main():
     steps = args.steps or DEFAULT_STEPS[args.workload]
 
     import torch
-    from leap_amd.attention import HipAttention
-
     if not torch.cuda.is_available():
         print("no HIP device", file=sys.stderr)
         sys.exit(1)
-    dev = torch.device("cuda:0")
-    L, nh, nkv, hd, theta, batch, ctx, sidx = WORKLOADS[args.workload]
-    Ts = contexts(args.workload)
-    seq_len = int(Ts.max())
-    att = HipAttention(nh, nkv, hd, seq_len, n_layers=L, rope_theta=theta, max_batch=batch)
-    if args.split:
-        att.set_split(args.split)
-    att.kv_fill_normal(SEED + sidx, 1.0 / np.sqrt(hd))
 
-    g = torch.Generator(device=dev)
-    g.manual_seed(SEED + sidx)
-    scale = 1.0 / np.sqrt(hd)
-    q = torch.randn(L, batch, nh * hd, device=dev, generator=g) * scale
-    k = torch.randn(L, batch, nkv * hd, device=dev, generator=g) * scale
-    v = torch.randn(L, batch, nkv * hd, device=dev, generator=g) * scale
-    out = torch.empty(L, batch, nh * hd, device=dev)
-    pos_dev = torch.tensor(Ts - 1, dtype=torch.int32, device=dev)
-    max_pos = int(Ts.max()) - 1
-    stream = torch.cuda.Stream(device=dev)
-    sp = stream.cuda_stream
-    ptrs = [(q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(), out[l].data_ptr()) for l in range(L)]
-
-    is_block = args.workload in BLOCK_WORKLOADS
-    weights = None
-    if is_block:
-        dim, kvd = nh * hd, nkv * hd
-        wrng = np.random.default_rng(SEED + sidx)
-        weights = (
-            (1.0 + 0.1 * wrng.standard_normal(dim)).astype(np.float32),
-            (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
-            (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
-            (wrng.standard_normal((kvd, dim)) / np.sqrt(dim)).astype(np.float32),
-            (wrng.standard_normal((dim, dim)) / np.sqrt(dim)).astype(np.float32),
-        )
-        if args.workload in Q8_WORKLOADS:
-            weights = (weights[0],) + tuple(quantize_groups(w, Q8_GROUP) for w in weights[1:])
-            for l in range(L):
-                att.set_layer_weights_q8(l, Q8_GROUP, *weights)
-        else:
-            for l in range(L):
-                att.set_layer_weights(l, *weights)
-        x_res = torch.randn(dim, device=dev, generator=g)
-        xp = x_res.data_ptr()
-        pos = int(Ts[0]) - 1
-
-        def one_step():
-            for l in range(L):
-                att.block_async(l, pos, xp, sp)
-    elif batch == 1:
-        pos = int(Ts[0]) - 1
-
-        def one_step():
-            for l in range(L):
-                qp, kp, vp, op = ptrs[l]
-                att.step_async(l, pos, qp, kp, vp, op, sp)
-    else:
-        pp = pos_dev.data_ptr()
-        total_rows = int(np.sum(Ts))
-
-        def one_step():
-            for l in range(L):
-                qp, kp, vp, op = ptrs[l]
-                att.step_batched_async(l, batch, pp, max_pos, qp, kp, vp, op, sp, total_rows)
-
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        one_step()
-    torch.cuda.synchronize()
-
-    # The timed region, cut into up to 10 segments by events on the same
-    # stream (for the spread); the total runs from the first event to the last.
-    n_seg = min(10, steps)
-    bounds = [round(i * steps / n_seg) for i in range(n_seg + 1)]
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_seg + 1)]
-    torch.cuda.synchronize()
-    evs[0].record(stream)
-    t0 = time.perf_counter()
-    for i in range(n_seg):
-        for _ in range(bounds[i + 1] - bounds[i]):
-            one_step()
-        evs[i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = evs[0].elapsed_time(evs[-1])
-    seg_us = np.array([evs[i].elapsed_time(evs[i + 1]) * 1e3 / ((bounds[i + 1] - bounds[i]) * L)
-                       for i in range(n_seg)])
-
-    launches = steps * L
-    us_layer = ms_total * 1e3 / launches
-    graph_us = None if args.no_graph else hip_graph_us(one_step, stream, steps, L)
-    is_q8 = args.workload in Q8_WORKLOADS
-    per_seq = q8_block_bytes if is_q8 else block_bytes if is_block else algorithmic_bytes
-    bytes_layer = int(sum(per_seq(int(T), nh, nkv, hd) for T in Ts))
-    gbs = bytes_layer / (us_layer * 1e-6) / 1e9
-    if not np.isfinite((x_res if is_block else out).float().sum().item()):
+    w = Workload(args.workload, split=args.split)
+    r = measure(w, steps, args.warmup, graph=not args.no_graph)
+    if not w.finite():
         print("non-finite output", file=sys.stderr)
         sys.exit(1)
-
+    us_layer, gbs = r["us_per_layer_step"], r["value"]
+    L, nh, nkv, hd, theta, batch = w.L, w.nh, w.nkv, w.hd, w.theta, w.batch
+    Ts = w.Ts
     result = {
-        "metric": Q8_METRIC if is_q8 else BLOCK_METRIC if is_block else METRIC,
-        "value": round(gbs, 2),
+        "metric": metric_for(args.workload),
+        "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_total / steps, 5),
+        "ms_per_step": round(r["ms_total"] / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8+f32" if is_q8 else "f32",
+        "dtype": "int8+f32" if w.is_q8 else "f32",
         "data": (f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache generated on the device; "
-                 f"N(0,1)/sqrt(dim) weights{f', int8 with one scale per {Q8_GROUP} values' if is_q8 else ''}, "
-                 f"one set uploaded into every layer)") if is_block else
+                 f"N(0,1)/sqrt(dim) weights{f', int8 with one scale per {Q8_GROUP} values' if w.is_q8 else ''}, "
+                 f"one set uploaded into every layer)") if w.is_block else
                 f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache and q/k/v, generated on the device)",
         "config": {
             "workload": args.workload, "n_layers": L, "n_heads": nh, "n_kv_heads": nkv,
@@ -530,47 +730,70 @@ def main():
             "context": int(Ts[0]) if batch == 1 else
             {"min": int(Ts.min()), "max": int(Ts.max()), "sum": int(Ts.sum())},
         },
-        "us_per_layer_step": round(us_layer, 3),
-        "us_per_layer_step_spread": {"segments": n_seg, "median": round(float(np.median(seg_us)), 3),
-                                     "p10": round(float(np.percentile(seg_us, 10)), 3),
-                                     "p90": round(float(np.percentile(seg_us, 90)), 3)},
+        "us_per_layer_step": us_layer,
+        "us_per_layer_step_spread": r["spread"],
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
         "tokens_layers_per_s": round(batch * 1e6 / us_layer, 1),
-        "host_wall_s": round(wall, 4),
+        "host_wall_s": round(r["wall"], 4),
         "roofline": {
-            "kernel": Q8_KERNELS if is_q8 else BLOCK_KERNELS if is_block else KERNEL,
+            "kernel": Q8_KERNELS if w.is_q8 else BLOCK_KERNELS if w.is_block else KERNEL,
             "bound": "hbm",
-            "achieved": round(gbs, 2),
+            "achieved": gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "frac": r["frac"],
             "traffic": traffic_from_profiles(args.workload),
-            "bytes_per_launch": bytes_layer,
-            "launch_us": round(us_layer, 3),
+            "traffic_source": f"profiles/decode_attention_{args.workload}_traffic.txt (rocprofv3 FETCH_SIZE and "
+                              "WRITE_SIZE of the same kernels, copy-scaled; counters need a run of their own)",
+            "bytes_per_launch": w.bytes_layer,
+            "launch_us": us_layer,
         },
         "cpu_baseline": None,
     }
-    if graph_us is not None:
+    if "hip_graph_us" in r:
+        gus = r["hip_graph_us"]
         result["hip_graph"] = {
-            "us_per_layer_step": round(graph_us, 3),
-            "value": round(bytes_layer / (graph_us * 1e-6) / 1e9, 2),
+            "us_per_layer_step": gus,
+            "value": round(w.bytes_layer / (gus * 1e-6) / 1e9, 2),
             "unit": "GB/s",
-            "note": "the same step captured once into a HIP graph and replayed; `value` above is eager launches",
+            "note": "the same steps captured into a HIP graph (at least 32 launches per graph) and replayed; "
+                    "`value` above is eager launches",
+        }
+    if not args.no_extra and not w.is_block:
+        fl = w.floor_us(1, steps, args.warmup)
+        fs = w.floor_us(2, steps, args.warmup)
+        kv_bytes = int(sum(8 * (int(T) - 1) * nkv * hd for T in Ts))
+        result["floor"] = {
+            "launch_us_per_layer_step": round(fl, 3),
+            "stream_us_per_layer_step": round(fs, 3),
+            "stream_GBps": round(kv_bytes / (fs * 1e-6) / 1e9, 1),
+            "kernel_over_stream_floor_us": round(us_layer - fs, 3),
+            "note": "the same grid, block and argument block as the step: a kernel that only reads its "
+                    "arguments (launch floor), and one that only streams the same K/V rows with the same "
+                    "loads and sums them (launch + bare stream); eager launches, events over the same steps",
         }
     if batch == 1 and not args.no_host_pointer:
-        result["host_pointer"] = host_pointer_rate(att, L, pos, bytes_layer, is_block,
+        pos = int(Ts[0]) - 1
+        result["host_pointer"] = host_pointer_rate(w.att, L, pos, w.bytes_layer, w.is_block,
                                                    sweeps=max(1, min(steps, 20)))
     if not args.no_cpu:
         try:
-            if is_block:
-                result["cpu_baseline"] = cpu_baseline_block(att, args.workload, Ts, args.cpu_layers,
-                                                            args.cpu_seconds, weights, q8=is_q8)
-            else:
-                result["cpu_baseline"] = cpu_baseline(att, args.workload, Ts, args.cpu_layers,
-                                                      args.cpu_seconds)
+            result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, args.cpu_layers)
         except Exception as e:  # the GPU line still stands; say why the CPU leg is missing
             result["cpu_baseline"] = {"error": f"{type(e).__name__}: {e}"}
-    att.close()
+    w.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    if not args.no_extra and args.workload == "llama3-8b-ctx4096":
+        result["workloads"] = {}
+        for name in EXTRA_WORKLOADS:
+            try:
+                result["workloads"][name] = extra_workload(name)
+            except Exception as e:
+                result["workloads"][name] = {"error": f"{type(e).__name__}: {e}"}
+            print(f"[bench] {name}: {result['workloads'][name].get('us_per_layer_step')} us/layer-step",
+                  file=sys.stderr, flush=True)
+        result["t_sweep"] = t_sweep()
     print(json.dumps(result), flush=True)
 
 

@@ -861,6 +861,72 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     }
 }
 
+// ---- launch and stream floors (measurement only) ----------------------------
+//
+// Two kernels with the decode kernel's grid, block size and argument, for
+// measuring what any one-launch design at a given shape must pay:
+//   - floor_launch_kernel reads two kernel arguments and exits (the launch,
+//     the argument load and the drain of an empty grid);
+//   - floor_stream_kernel streams the same K and V rows with the same loads
+//     (128-bit, non-temporal, the same lane layout and passes) and only sums
+//     them (the launch plus the bare stream of the step's bytes).
+// Neither writes anything: the sums are kept only behind a test that real
+// data never meets (a NaN with a particular payload).
+
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * kWave) void floor_launch_kernel(StepArgs a)
+{
+    if (a.grid_chunks < 0 && a.n_groups < 0) a.out[threadIdx.x] = 0.0f;
+}
+
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
+{
+    using S = Shape<HD, G, NW>;
+    constexpr int NF = S::NF, R = S::R, KS = S::KS, LPV = S::LPV, RPV = S::RPV, VS = S::VS;
+    const int xcd = blockIdx.x % kXcds;
+    const int local = blockIdx.x / kXcds;
+    const int chunk_id = local % a.grid_chunks;
+    const int group = (local / a.grid_chunks) * kXcds + xcd;
+    if (group >= a.n_groups) return;
+    const int seq = group / a.n_kv_heads;
+    const int kvh = group % a.n_kv_heads;
+    const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
+    if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
+    const int T = pos + 1;
+    const int n_chunks = (T + a.chunk - 1) / a.chunk;
+    if (chunk_id >= n_chunks) return;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const uint32_t row_bytes = (uint32_t)(a.n_kv_heads * HD) * 4u;
+    const size_t slab = (size_t)seq * (size_t)a.seq_stride;
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k_cache + slab + (size_t)kvh * HD, (uint32_t)pos * row_bytes);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v_cache + slab + (size_t)kvh * HD, (uint32_t)pos * row_bytes);
+    const int kj = lane & 3, ksl = (lane >> 2) & 7, kq = lane >> 5, krow = 4 * kq + kj;
+    const int vg = lane / LPV, vj = lane % LPV;
+    const int chunk_begin = chunk_id * a.chunk;
+    const int n_sub = (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
+    float sum = 0.0f;
+    for (int sub = 0; sub < n_sub; sub++) {
+        const int base = chunk_begin + (sub * NW + wave) * R;
+        float4 kb[KS][NF], vb[VS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int f = 0; f < NF; f++)
+                kb[ks][f] = buf_load4<kNt>(k_rsrc, (uint32_t)(base + ks * 8 + krow) * row_bytes + 16u * (uint32_t)(8 * f + ksl));
+#pragma unroll
+        for (int vs = 0; vs < VS; vs++)
+            vb[vs] = buf_load4<kNt>(v_rsrc, (uint32_t)(base + vs * RPV + vg) * row_bytes + 16u * (uint32_t)vj);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (int f = 0; f < NF; f++) sum += kb[ks][f].x + kb[ks][f].y + kb[ks][f].z + kb[ks][f].w;
+#pragma unroll
+        for (int vs = 0; vs < VS; vs++) sum += vb[vs].x + vb[vs].y + vb[vs].z + vb[vs].w;
+    }
+    if (__builtin_bit_cast(unsigned, sum) == 0x7FC0DEADu) a.out[threadIdx.x] = sum;
+}
+
 // ---- placement probe ---------------------------------------------------------
 
 // The XCC (XCD) each workgroup runs on, from the hardware register XCC_ID

@@ -131,10 +131,17 @@ using KernelFn = void (*)(leap::StepArgs);
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * leap::kWave;
 
-KernelFn pick_kernel(int hd, int g)
+// What a launch runs: the decode kernel, or one of the floor kernels with its
+// grid (measurement only).
+enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
+
+KernelFn pick_kernel(int hd, int g, int kind = kDecode)
 {
-#define LEAP_CASE(HD, G) \
-    if (hd == HD && g == G) return leap::decode_attention_kernel<HD, G, kWaves>;
+#define LEAP_CASE(HD, G)                                                                  \
+    if (hd == HD && g == G)                                                               \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>          \
+               : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>          \
+                                      : leap::decode_attention_kernel<HD, G, kWaves>;
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
@@ -226,10 +233,10 @@ int max_chunks_for(int seq_len, int head_dim, int group, int cap)
 // (hipErrorInvalidValue for a shape without a kernel or a launch too large).
 hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_seq, const int *pos_dev,
                             int pos_scalar, int max_pos, long long total_rows, const float *q, const float *k,
-                            const float *v, float *out, hipStream_t stream)
+                            const float *v, float *out, hipStream_t stream, int kind = kDecode)
 {
     const int hd = s.head_dim;
-    KernelFn fn = pick_kernel(hd, s.group);
+    KernelFn fn = pick_kernel(hd, s.group, kind);
     if (!fn) return hipErrorInvalidValue;
     const int chunk = choose_chunk(s, n_seq, total_rows, max_pos + 1);
     const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
@@ -272,7 +279,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
 
 int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
            int max_pos, long long total_rows, const float *q, const float *k, const float *v,
-           float *out, hipStream_t stream)
+           float *out, hipStream_t stream, int kind = kDecode)
 {
     if (!pick_kernel(h->cfg.head_dim, h->group))
         return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", h->cfg.head_dim, h->group);
@@ -280,7 +287,7 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
     const LaunchBuffers b{h->k_cache + loff, h->v_cache + loff, (long long)h->slab_floats, h->rope,
                           h->ws_o,           h->ws_ml,          h->counters};
     HIP_TRY(h, launch_attention(shape_of(h), b, n_seq, pos_dev, pos_scalar, max_pos, total_rows, q, k, v, out,
-                                stream));
+                                stream, kind));
     return 0;
 }
 
@@ -1165,6 +1172,24 @@ int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int p
         sin_out[i] = packed[2 * i + 1];
     }
     return 0;
+}
+
+int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, int max_pos,
+                                   long long total_rows, void *stream)
+{
+    if (!h) return -EINVAL;
+    if (kind != kFloorLaunch && kind != kFloorStream) return set_err(h, -EINVAL, "floor kind %d is not 1 or 2", kind);
+    if (int rc = check_layer(h, layer)) return rc;
+    if (n_seq <= 0 || n_seq > h->cfg.max_batch)
+        return set_err(h, -EINVAL, "n_seq %d outside [1, %d]", n_seq, h->cfg.max_batch);
+    if (max_pos < 0 || max_pos >= h->cfg.seq_len)
+        return set_err(h, -EINVAL, "max_pos %d outside [0, %d)", max_pos, h->cfg.seq_len);
+    if (total_rows <= 0 || total_rows > (long long)n_seq * (max_pos + 1))
+        return set_err(h, -EINVAL, "total_rows %lld outside [1, %lld]", total_rows, (long long)n_seq * (max_pos + 1));
+    HIP_TRY(h, hipSetDevice(h->cfg.device));
+    // every sequence at max_pos (the kernels read no positions array)
+    return launch(h, layer, n_seq, nullptr, max_pos, max_pos, total_rows, nullptr, nullptr, nullptr, h->out_dev,
+                  (hipStream_t)stream, kind);
 }
 
 int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions)

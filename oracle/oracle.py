@@ -20,8 +20,11 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle_attn.so")
-REF_SO = os.path.join(HERE, "_ref", "libleap_ref.so")
-REF_Q8_SO = os.path.join(HERE, "_ref", "libleap_ref_q8.so")
+# LEAP_REF_VARIANT=v4 selects the reference timing libraries built for an
+# AVX-512 target (the CPU-baseline leg sets it on AVX-512 hosts).
+_VARIANT = "_v4" if os.environ.get("LEAP_REF_VARIANT") == "v4" else ""
+REF_SO = os.path.join(HERE, "_ref", f"libleap_ref{_VARIANT}.so")
+REF_Q8_SO = os.path.join(HERE, "_ref", f"libleap_ref_q8{_VARIANT}.so")
 REF_CKPT_SO = os.path.join(HERE, "_ref", "libleap_ref_ckpt.so")
 REF_SRC = "/root/reference/src/inference"
 

@@ -93,3 +93,24 @@ def test_async_on_a_caller_stream_then_clear_and_step():
         k_slot, v_slot = att.kv_download(0, 0, 3000, 3001)
         assert np.array_equal(k_slot[0], orc.key_cache[0, 3000])
         assert np.array_equal(v_slot[0], orc.value_cache[0, 3000])
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_floor_launches_write_nothing(kind):
+    """The measurement launches (launch floor, bare stream floor) with a real
+    step's shape leave the cache and the step's output untouched."""
+    import torch
+    nh, nkv, hd, T = 32, 8, 128, 2048
+    with HipAttention(nh, nkv, hd, T, n_layers=2, max_batch=3) as att:
+        att.kv_fill_normal(93, 1.0 / np.sqrt(hd))
+        k0, v0 = att.kv_download(2, 1, 0, T)
+        s = torch.cuda.Stream()
+        att.floor_async(kind, 1, 1, T - 1, T, s.cuda_stream)
+        att.floor_async(kind, 1, 3, 1000, 3 * 1001, s.cuda_stream)
+        s.synchronize()
+        k1, v1 = att.kv_download(2, 1, 0, T)
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+        with pytest.raises(LeapError):
+            att.floor_async(3, 1, 1, T - 1, T, s.cuda_stream)
+        with pytest.raises(LeapError):
+            att.floor_async(kind, 1, 4, T - 1, T, s.cuda_stream)
