@@ -247,7 +247,7 @@ class Workload:
     """One configuration on the device: the handle, its filled cache, the
     step's inputs, and one_step() running the layer sweep on `stream`."""
 
-    def __init__(self, workload: str, split: int = 0):
+    def __init__(self, workload: str, split: int = 0, valu: bool = False):
         import torch
         from leap_amd.attention import HipAttention
         self.name = workload
@@ -261,6 +261,8 @@ class Workload:
                                       max_batch=batch)
         if split:
             att.set_split(split)
+        if valu:
+            att.set_products(True)
         att.kv_fill_normal(SEED + sidx, 1.0 / np.sqrt(hd))
         g = torch.Generator(device=dev)
         g.manual_seed(SEED + sidx)
@@ -668,6 +670,8 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=4)
     ap.add_argument("--split", type=int, default=0, help="positions per split-K chunk (0 = auto)")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay timing")
+    ap.add_argument("--products", choices=("mfma", "valu"), default="mfma",
+                    help="score and weighted-V products on the matrix cores (default) or the VALU")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -700,7 +704,7 @@ def main():
         print("no HIP device", file=sys.stderr)
         sys.exit(1)
 
-    w = Workload(args.workload, split=args.split)
+    w = Workload(args.workload, split=args.split, valu=args.products == "valu")
     r = measure(w, steps, args.warmup, graph=not args.no_graph)
     if not w.finite():
         print("non-finite output", file=sys.stderr)
@@ -720,6 +724,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8+f32" if w.is_q8 else "f32",
+        "products": args.products,
         "data": (f"synthetic (seeded N(0,1)/sqrt({hd}) KV cache generated on the device; "
                  f"N(0,1)/sqrt(dim) weights{f', int8 with one scale per {Q8_GROUP} values' if w.is_q8 else ''}, "
                  f"one set uploaded into every layer)") if w.is_block else
@@ -771,6 +776,17 @@ def main():
             "note": "the same grid, block and argument block as the step: a kernel that only reads its "
                     "arguments (launch floor), and one that only streams the same K/V rows with the same "
                     "loads and sums them (launch + bare stream); eager launches, events over the same steps",
+        }
+    if not args.no_extra and not w.is_block:
+        # the A/B of the matrix-core choice: the same launches with the products on the VALU
+        w.att.set_products(args.products == "mfma")
+        rv = measure(w, steps, args.warmup, graph=False)
+        w.att.set_products(args.products == "valu")
+        other = "valu" if args.products == "mfma" else "mfma"
+        result["products_ab"] = {
+            f"{args.products}_us_per_layer_step": us_layer, f"{other}_us_per_layer_step": rv["us_per_layer_step"],
+            "note": "score (q.K) and weighted-V products on the matrix cores (4x4x1 f32 MFMA) or as per-lane "
+                    "VALU FMAs with the same cross-lane sums; same launches, same events",
         }
     if batch == 1 and not args.no_host_pointer:
         pos = int(Ts[0]) - 1

@@ -303,6 +303,12 @@ int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int p
  * choice; otherwise a multiple of 64.  A tuning and test knob. */
 int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions);
 
+/* Where later steps compute the score (q . K) and weighted-V products: 0 on
+ * the matrix cores (4x4x1 f32 MFMAs, the default), 1 as per-lane VALU FMAs
+ * with the same cross-lane sums.  Both give results within the same bar of
+ * the reference; a measurement knob for the A/B of the matrix-core choice. */
+int leap_hip_attention_set_products(leap_hip_attention *h, int valu);
+
 /* Device addresses of the (seq, layer) cache slabs, for callers that keep
  * their own device-side views of the cache. */
 int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,

@@ -37,6 +37,7 @@ EXPORTS = (
     "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
     "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
     "leap_hip_attention_xcc_map", "leap_hip_attention_step_noalloc", "leap_hip_attention_floor_async",
+    "leap_hip_attention_set_products",
 )
 
 PACKET_HEADER_BYTES = 8
@@ -113,6 +114,7 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_packet_download.argtypes = [H, _P, _I, _I, _P, ctypes.c_size_t, _P]
     L.leap_hip_attention_xcc_map.argtypes = [_I, _I, ctypes.POINTER(_I)]
     L.leap_hip_attention_floor_async.argtypes = [H, _I, _I, _I, _I, ctypes.c_longlong, _P]
+    L.leap_hip_attention_set_products.argtypes = [H, _I]
     L.leap_hip_attention_step_noalloc.argtypes = [ctypes.POINTER(Config), _I] + [_P] * 8
     for name in EXPORTS:
         fn = getattr(L, name)
@@ -345,6 +347,10 @@ class HipAttention:
         """Enqueue a floor launch of a step's shape: kind 1 launch only,
         kind 2 the bare K/V stream (measurement; writes nothing)."""
         self._check(self.lib.leap_hip_attention_floor_async(self.h, kind, layer, n_seq, max_pos, total_rows, stream))
+
+    def set_products(self, valu: bool):
+        """Score and weighted-V products on the VALU (True) or the matrix cores."""
+        self._check(self.lib.leap_hip_attention_set_products(self.h, 1 if valu else 0))
 
     def set_split(self, chunk_positions):
         self._check(self.lib.leap_hip_attention_set_split(self.h, chunk_positions))

@@ -281,7 +281,10 @@ struct Shape {
     static_assert(MG >= 1 && THREADS % (GM * D4) == 0, "merge layout");
 };
 
-template <int HD, int G, int NW>
+// MFMA: the score and weighted-V products on the matrix cores (4x4x1 f32
+// MFMAs); false: the same products as per-lane VALU FMAs, leaving the same
+// partial sums in the same lanes (the A/B of the matrix-core choice).
+template <int HD, int G, int NW, bool MFMA = true>
 __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
@@ -477,8 +480,22 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
             for (int qd = 0; qd < GQ; qd++) {
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (MFMA) {
 #pragma unroll
-                for (int f = 0; f < NF; f++) d = mfma4(qa[qd][f], kb[ks][f], d);
+                    for (int f = 0; f < NF; f++) d = mfma4(qa[qd][f], kb[ks][f], d);
+                } else {
+                    // lane (kq, ksl, kj): head 4*qd + i times row 4*kq + kj over
+                    // this lane's dims, the partial the MFMA leaves in d[i]
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (4 * qd + i >= G) continue;
+#pragma unroll
+                        for (int f = 0; f < NF; f++) {
+                            const float4 qv = q_lds[4 * qd + i][8 * f + ksl];
+                            d[i] += qv.x * kb[ks][f].x + qv.y * kb[ks][f].y + qv.z * kb[ks][f].z + qv.w * kb[ks][f].w;
+                        }
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     if (4 * qd + i >= G) continue;
@@ -554,12 +571,25 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             }
 #pragma unroll
             for (int q = 0; q < GQ; q++) {
-                const int h = 4 * q + (lane & 3);
-                const float pa = (h < G) ? p_lds[wave][r * G + h] : 0.0f;
-                acc[q][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].x, acc[q][0], 0, 0, 0);
-                acc[q][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].y, acc[q][1], 0, 0, 0);
-                acc[q][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].z, acc[q][2], 0, 0, 0);
-                acc[q][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].w, acc[q][3], 0, 0, 0);
+                if constexpr (MFMA) {
+                    const int h = 4 * q + (lane & 3);
+                    const float pa = (h < G) ? p_lds[wave][r * G + h] : 0.0f;
+                    acc[q][0] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].x, acc[q][0], 0, 0, 0);
+                    acc[q][1] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].y, acc[q][1], 0, 0, 0);
+                    acc[q][2] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].z, acc[q][2], 0, 0, 0);
+                    acc[q][3] = __builtin_amdgcn_mfma_f32_4x4x1f32(pa, vb[vs].w, acc[q][3], 0, 0, 0);
+                } else {
+                    // acc[q][e][i]: head 4q+i at dim 4*vj + e, as the MFMA leaves it
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        if (4 * q + i >= G) continue;
+                        const float pa = p_lds[wave][r * G + 4 * q + i];
+                        acc[q][0][i] += pa * vb[vs].x;
+                        acc[q][1][i] += pa * vb[vs].y;
+                        acc[q][2][i] += pa * vb[vs].z;
+                        acc[q][3][i] += pa * vb[vs].w;
+                    }
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();

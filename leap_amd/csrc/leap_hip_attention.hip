@@ -74,6 +74,7 @@ struct leap_hip_attention {
     int split = 0;
     int n_cu = 256;  // compute units of the device
     int max_chunks = 1;  // chunks per sequence the workspace holds records for
+    bool valu = false;   // score and weighted-V products on the VALU (measurement knob)
     std::string err;
 };
 
@@ -135,13 +136,14 @@ constexpr int kThreads = kWaves * leap::kWave;
 // grid (measurement only).
 enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
 
-KernelFn pick_kernel(int hd, int g, int kind = kDecode)
+KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false)
 {
 #define LEAP_CASE(HD, G)                                                                  \
     if (hd == HD && g == G)                                                               \
         return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>          \
                : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>          \
-                                      : leap::decode_attention_kernel<HD, G, kWaves>;
+               : valu                 ? leap::decode_attention_kernel<HD, G, kWaves, false> \
+                                      : leap::decode_attention_kernel<HD, G, kWaves, true>;
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
@@ -166,6 +168,7 @@ struct LaunchShape {
     int n_cu;
     int split;
     int max_chunks;
+    bool valu = false;  // products as VALU FMAs instead of MFMAs (the A/B knob)
 };
 
 // The device buffers of one launch (one layer): the cache slabs of sequence
@@ -184,7 +187,7 @@ struct LaunchBuffers {
 LaunchShape shape_of(const leap_hip_attention *h)
 {
     return LaunchShape{h->cfg.head_dim, h->group, h->cfg.n_heads, h->cfg.n_kv_heads, h->cfg.seq_len,
-                       h->n_cu, h->split, h->max_chunks};
+                       h->n_cu, h->split, h->max_chunks, h->valu};
 }
 
 // Positions per workgroup (chunk), from the size and shape of the launch:
@@ -236,7 +239,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
                             const float *v, float *out, hipStream_t stream, int kind = kDecode)
 {
     const int hd = s.head_dim;
-    KernelFn fn = pick_kernel(hd, s.group, kind);
+    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu);
     if (!fn) return hipErrorInvalidValue;
     const int chunk = choose_chunk(s, n_seq, total_rows, max_pos + 1);
     const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
@@ -1190,6 +1193,14 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
     // every sequence at max_pos (the kernels read no positions array)
     return launch(h, layer, n_seq, nullptr, max_pos, max_pos, total_rows, nullptr, nullptr, nullptr, h->out_dev,
                   (hipStream_t)stream, kind);
+}
+
+int leap_hip_attention_set_products(leap_hip_attention *h, int valu)
+{
+    if (!h) return -EINVAL;
+    if (valu != 0 && valu != 1) return set_err(h, -EINVAL, "products mode %d is not 0 (MFMA) or 1 (VALU)", valu);
+    h->valu = valu == 1;
+    return 0;
 }
 
 int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions)

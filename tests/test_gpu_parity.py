@@ -102,6 +102,24 @@ def test_step_shapes_and_splits(nh, nkv, hd, T, split):
         assert not k0.any() and not v0.any()
 
 
+@pytest.mark.parametrize("nh,nkv,hd", SHAPES)
+@pytest.mark.parametrize("T,split", [(1, 0), (65, 64), (1000, 64), (4096, 64), (2049, 0)])
+def test_valu_products_shapes_and_splits(nh, nkv, hd, T, split):
+    """The score and weighted-V products as VALU FMAs (the measurement knob
+    set_products) meet the same bar, and write the same cache rows."""
+    theta = 10000.0 if hd == 64 else 500000.0
+    rng = rng_for(nh, nkv, hd, T, split, 1)
+    with HipAttention(nh, nkv, hd, T + 5, rope_theta=theta) as att:
+        att.set_products(True)
+        if split:
+            att.set_split(split)
+        pos = T - 1
+        att.kv_upload(0, 0, 0, normal(rng, (pos, nkv * hd), hd), normal(rng, (pos, nkv * hd), hd))
+        q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+        out = att.step(0, pos, q, k, v)
+        _step_and_check(att, 0, pos, q, k, v, theta, out=out)
+
+
 def test_first_position_returns_v_exactly():
     with HipAttention(32, 8, 128, 16) as att:
         rng = rng_for(5)
