@@ -14,6 +14,7 @@
 #include "checkpoint.hpp"
 
 #include <cerrno>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -123,6 +124,8 @@ extern "C" int leap_hip_attention_checkpoint_read(const char *path, leap_hip_att
     c.vocab_size = cfg[5];
     c.seq_len = cfg[6];
     if (c.version != 2) {
+        // (the most negative int has no magnitude in int: not a vocabulary size)
+        if (c.vocab_size == INT32_MIN) return -EINVAL;
         c.shared_classifier = c.vocab_size > 0 ? 1 : 0;
         c.vocab_size = std::abs(c.vocab_size);
     }
@@ -133,6 +136,8 @@ extern "C" int leap_hip_attention_checkpoint_read(const char *path, leap_hip_att
     leap::CkptLayer lay;
     size_t needed;
     if (!leap::ckpt_layer(c, 0, &lay, &needed)) return -EINVAL;
+    // reported as a signed count: larger than any file can be is not a model
+    if (needed > (size_t)INT64_MAX) return -EINVAL;
     c.attention_bytes = (long long)needed;
     *out = c;
     return 0;

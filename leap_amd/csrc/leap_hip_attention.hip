@@ -1226,7 +1226,7 @@ int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path)
         return set_err(h, -EINVAL, "%s: model %d layers, %d/%d heads, dim %d; the handle holds %d layers, %d/%d heads of %d",
                        path, c.n_layers, c.n_heads, c.n_kv_heads, c.dim, hc.n_layers, hc.n_heads, hc.n_kv_heads,
                        hc.head_dim);
-    if (c.file_bytes < c.attention_bytes)
+    if (c.attention_bytes < c.header_bytes || c.file_bytes < c.attention_bytes)
         return set_err(h, -EINVAL, "%s: %lld bytes, the attention weights need %lld", path, c.file_bytes,
                        c.attention_bytes);
     const int fd = open(path, O_RDONLY);

@@ -17,14 +17,15 @@ extern "C" void leap_rope_table_host(int seq_len, int head_size, float theta, fl
 {
     const int half = head_size / 2;
     for (int pos = 0; pos < seq_len; pos++) {
-        for (int i = 0; i < head_size; i += 2) {
+        for (int j = 0; j < half; j++) {  // the even i of the reference's loop, one table entry each
+            const int i = 2 * j;
             float freq;
             if (theta == 500000.0f)
                 freq = 1.0f / std::pow(500000.0f, static_cast<float>(i) / static_cast<float>(head_size));
             else
                 freq = 1.0f / std::pow(theta, static_cast<float>(i) / static_cast<float>(head_size));
             const float val = static_cast<float>(pos) * freq;
-            const size_t idx = static_cast<size_t>(pos) * half + static_cast<size_t>(i / 2);
+            const size_t idx = static_cast<size_t>(pos) * half + static_cast<size_t>(j);
             cos_tab[idx] = std::cos(val);
             sin_tab[idx] = std::sin(val);
         }

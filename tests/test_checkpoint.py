@@ -150,3 +150,15 @@ def test_load_checkpoint_rejects_mismatches(tmp_path, hip_device):
             att.load_checkpoint(tmp_path / "missing.bin")
         with pytest.raises(A.LeapError):  # nothing was uploaded by the failed loads
             att.block(0, 0, np.zeros(dim, np.float32))
+
+
+@pytest.mark.parametrize("cfg", [
+    (256, 64, 2, 4, 2, -2**31, 16),            # vocab_size INT_MIN: no magnitude (the fuzz's UBSan finding)
+    (2**31 - 1, 64, 2**31 - 1, 1, 1, 8, 16),   # tensor bytes beyond any signed file size
+])
+def test_header_rejects_unrepresentable_sizes(tmp_path, cfg):
+    import struct
+    path = tmp_path / "x.bin"
+    path.write_bytes(struct.pack("<7i", *cfg) + bytes(64))
+    with pytest.raises(A.LeapError):
+        A.checkpoint_read(path)
