@@ -373,6 +373,7 @@ def extra_workload(name: str):
     try:
         r = measure(w, steps, 3)
         ok = w.finite()
+        floor = w.floor_us(2, steps, 3) if not w.is_block else None
     finally:
         w.close()
         torch.cuda.synchronize()
@@ -388,6 +389,8 @@ def extra_workload(name: str):
                    "rope_theta": theta,
                    "context": int(Ts[0]) if batch == 1 else {"min": int(Ts.min()), "max": int(Ts.max()),
                                                              "sum": int(Ts.sum())}},
+        "stream_floor_us_per_layer_step": round(floor, 3) if floor else None,
+        "stream_floor_frac": round(r["bytes_per_launch"] / (floor * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if floor else None,
         "finite": ok,
     }
 
