@@ -143,10 +143,11 @@ int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, in
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).  The split-K workspace is
  * a 4 MiB static device array, one per device (held until the process ends):
- * a fixed 144 KiB region of arrival counters (n_kv_heads <= 128), then
- * n_heads x 72 partial records of (head_dim + 2) floats, at most 64 split-K
- * chunks per call (up to 108 heads of 128 or 212 heads of 64; Llama-3-8B
- * uses 1.35 MB, Llama-3-70B 2.54 MB); larger shapes return -EINVAL.  Every
+ * a fixed 144 KiB region of arrival counters (n_kv_heads <= 128) and 33 KiB
+ * of part records, then n_heads x 72 partial records of (head_dim + 2)
+ * floats (for at least 8 KV heads' worth of q heads), at most 64 split-K
+ * chunks per call (up to 107 heads of 128 or 211 heads of 64; Llama-3-8B
+ * uses 1.38 MB, Llama-3-70B 2.58 MB); larger shapes return -EINVAL.  Every
  * call on one device shares that array: launches leave the counters at
  * zero and the first call on a device clears the array on its stream, so
  * calls that overlap on one GPU, on any streams, race.

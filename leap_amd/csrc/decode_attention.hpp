@@ -104,6 +104,10 @@ struct StepArgs {
     float scale_log2;    // log2(e) / sqrt(HD)
     int merge_asym;      // every CU runs two one-pass workgroups of the launch: the
                          // first-dispatched half of a group's chunks finishes first
+    int spread_log2;     // a group's chunks are cut into 2^spread_log2 parts on as many
+                         // XCDs (launches of fewer groups than XCDs); 0: one part
+    float *ws_po;        // [n_groups << spread_log2][G][HD] each part's unnormalised output
+    float2 *ws_pml;      // [n_groups << spread_log2][G] its (max, sum), log2 units
 };
 
 // ---- buffer access ------------------------------------------------------------
@@ -291,12 +295,18 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
     constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, GM = S::GM, MG = S::MG;
 
-    // id = ((group / 8) * grid_chunks + chunk) * 8 + group % 8
+    // id = ((pg / 8) * grid_chunks + lc) * 8 + pg % 8, where the part-group
+    // pg = group * 2^spread_log2 + part covers the group's chunks
+    // [part * grid_chunks, (part + 1) * grid_chunks) and lc is the chunk
+    // within the part.  Every workgroup of a part-group runs on one XCD.
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
-    const int chunk_id = local % a.grid_chunks;
-    const int group = (local / a.grid_chunks) * kXcds + xcd;
-    if (group >= a.n_groups) return;
+    const int lc = local % a.grid_chunks;
+    const int pgroup = (local / a.grid_chunks) * kXcds + xcd;
+    if (pgroup >= (a.n_groups << a.spread_log2)) return;
+    const int group = pgroup >> a.spread_log2;
+    const int part = pgroup & ((1 << a.spread_log2) - 1);
+    const int chunk_id = part * a.grid_chunks + lc;  // within the group
     const int seq = group / a.n_kv_heads;
     const int kvh = group % a.n_kv_heads;
     const int tid = threadIdx.x;
@@ -308,6 +318,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const int T = pos + 1;
     const int n_chunks = (T + a.chunk - 1) / a.chunk;
     if (chunk_id >= n_chunks) return;
+    // chunks of this part (at least 1 here)
+    const int n_local = min(a.grid_chunks, n_chunks - part * a.grid_chunks);
 
     const int kv_dim = a.n_kv_heads * HD;
     const int q_dim = a.n_heads * HD;
@@ -611,9 +623,21 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     __syncthreads();
 
     // Combine the waves: one float4 of one head per thread.
-    const bool single = (n_chunks == 1);
+    const bool single = (n_local == 1);
     const int n_rec = records_per_head(a.grid_chunks);
-    const size_t ws_head0 = ((size_t)seq * a.n_heads + (size_t)kvh * G) * (size_t)n_rec;
+    const size_t ws_head0 = (size_t)pgroup * G * (size_t)n_rec;
+    // A part-group's finished result: the output row (one part), or the
+    // part's unnormalised record for the cross-XCD merge launch.
+    const bool parts = a.spread_log2 > 0;
+    auto emit = [&](int head, int col, float4 o, float M, float L) {
+        if (parts) {
+            reinterpret_cast<float4 *>(a.ws_po + ((size_t)pgroup * G + head) * HD)[col] = o;
+            if (col == 0) a.ws_pml[(size_t)pgroup * G + head] = make_float2(M, L);
+        } else {
+            scale4(o, 1.0f / L);
+            reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + head) * HD)[col] = o;
+        }
+    };
     const uint32_t ws_o_bytes = (uint32_t)(G * n_rec * HD) * 4u;
     const uint32_t ws_ml_bytes = (uint32_t)(G * n_rec) * 8u;
     const __amdgpu_buffer_rsrc_t wo_rsrc = make_rsrc(a.ws_o + ws_head0 * HD, ws_o_bytes);
@@ -633,11 +657,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             L += sc * comb_l[w][ch];
         }
         if (single) {
-            scale4(o, 1.0f / L);
-            reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + ch) * HD)[cd4] = o;
+            emit(ch, cd4, o, M, L);
         } else {
             // Partial o and (max, sum), into this XCD's L2.
-            const uint32_t row = (uint32_t)(ch * n_rec + chunk_id);
+            const uint32_t row = (uint32_t)(ch * n_rec + lc);
             buf_store4(wo_rsrc, row * (HD * 4u) + 16u * cd4, o);
             if (cd4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(M, L));
         }
@@ -784,8 +807,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
             }
         }
     };
-    int *ctr = a.counters + ((size_t)seq * a.n_kv_heads + kvh) * (size_t)counters_per_group(a.grid_chunks);
-    float4 *out_row = reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + mh) * HD);
+    int *ctr = a.counters + (size_t)pgroup * (size_t)counters_per_group(a.grid_chunks);
 
     // The asymmetric merge (see the header), for NC chunks: chunks [0, NC/2)
     // fold in sub-groups whose records go right after the chunk records, and
@@ -794,8 +816,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // exact.
     auto merge_asym = [&](auto nc_c) {
         constexpr int NC = decltype(nc_c)::value, half = NC / 2, n_final = half + half / kSubGroup;
-        if (chunk_id < half) {
-            const int sg1 = chunk_id / kSubGroup;
+        if (lc < half) {
+            const int sg1 = lc / kSubGroup;
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (tid == 0) {
@@ -827,28 +849,25 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         float4 of;
         float Mf, Lf;
         fold_wide(half, std::integral_constant<int, n_final>{}, of, Mf, Lf);
-        if (mg == 0 && live) {
-            scale4(of, 1.0f / Lf);
-            out_row[md4] = of;
-        }
+        if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
     };
     if (a.merge_asym) {
         if constexpr (32 + 4 <= MG * BW) {
-            if (n_chunks == 64) return merge_asym(std::integral_constant<int, 64>{});
+            if (n_local == 64) return merge_asym(std::integral_constant<int, 64>{});
         }
         if constexpr (24 + 3 <= MG * BW) {
-            if (n_chunks == 48) return merge_asym(std::integral_constant<int, 48>{});
+            if (n_local == 48) return merge_asym(std::integral_constant<int, 48>{});
         }
         if constexpr (16 + 2 <= MG * BW) {
-            if (n_chunks == 32) return merge_asym(std::integral_constant<int, 32>{});
+            if (n_local == 32) return merge_asym(std::integral_constant<int, 32>{});
         }
     }
 
     // Level 1: once this workgroup's partials have reached L2 (stores
     // drained), count it in on its sub-group's counter (an L2 atomic).
-    const int sg = chunk_id / kSubGroup;
-    const int n_sg = (n_chunks + kSubGroup - 1) / kSubGroup;
-    const int sg_n = min(kSubGroup, n_chunks - sg * kSubGroup);
+    const int sg = lc / kSubGroup;
+    const int n_sg = (n_local + kSubGroup - 1) / kSubGroup;
+    const int sg_n = min(kSubGroup, n_local - sg * kSubGroup);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -862,10 +881,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     float Mx, Lx;
     fold(sg * kSubGroup, sg_n, ox, Mx, Lx);
     if (n_sg == 1) {
-        if (mg == 0 && live) {
-            scale4(ox, 1.0f / Lx);
-            out_row[md4] = ox;
-        }
+        if (mg == 0 && live) emit(mh, md4, ox, Mx, Lx);
         return;
     }
     if (mg == 0 && live) {
@@ -885,10 +901,40 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     if (!s_last) return;
     if (tid == 0) ctr[0] = 0;
     fold(a.grid_chunks, n_sg, ox, Mx, Lx);
-    if (mg == 0 && live) {
-        scale4(ox, 1.0f / Lx);
-        out_row[md4] = ox;
+    if (mg == 0 && live) emit(mh, md4, ox, Mx, Lx);
+}
+
+// The cross-XCD merge of a spread launch: after the decode launch, the parts
+// of each (sequence, KV head) group have left one unnormalised record each
+// (the launch boundary makes them visible to every XCD).  One workgroup per
+// group, one thread per (q head, float4 column): fold the group's non-empty
+// parts in part order with an online max, normalise, write the output row.
+template <int HD, int G>
+__global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
+{
+    constexpr int D4 = HD / 4;
+    const int group = blockIdx.x;
+    if (group >= a.n_groups) return;
+    const int seq = group / a.n_kv_heads, kvh = group % a.n_kv_heads;
+    const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
+    if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
+    const int n_chunks = (pos + 1 + a.chunk - 1) / a.chunk;
+    const int n_parts = min(1 << a.spread_log2, (n_chunks + a.grid_chunks - 1) / a.grid_chunks);
+    const int h = threadIdx.x / D4, c = threadIdx.x % D4;
+    const size_t pg0 = (size_t)group << a.spread_log2;
+    float M = -INFINITY;
+    for (int p = 0; p < n_parts; p++) M = fmaxf(M, a.ws_pml[(pg0 + p) * G + h].x);
+    float L = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int p = 0; p < n_parts; p++) {
+        const float2 ml = a.ws_pml[(pg0 + p) * G + h];
+        const float w = (ml.x == -INFINITY) ? 0.f : fast_exp2(ml.x - M);
+        fma4(o, w, reinterpret_cast<const float4 *>(a.ws_po + ((pg0 + p) * G + h) * HD)[c]);
+        L += w * ml.y;
     }
+    scale4(o, 1.0f / L);
+    const int q_dim = a.n_heads * HD;
+    reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + h) * HD)[c] = o;
 }
 
 // ---- launch and stream floors (measurement only) ----------------------------

@@ -44,6 +44,8 @@ struct leap_hip_attention {
     float *ws_o = nullptr;
     float2 *ws_ml = nullptr;
     int *counters = nullptr;
+    float *ws_po = nullptr;    // part records of spread launches: [kXcds][group][head_dim]
+    float2 *ws_pml = nullptr;  // [kXcds][group]
     size_t counter_bytes = 0;
     // The host-pointer entry points stage their inputs through one pinned
     // host buffer and one device region (q rows | k rows | v rows | pos, packed
@@ -169,6 +171,7 @@ struct LaunchShape {
     int split;
     int max_chunks;
     bool valu = false;  // products as VALU FMAs instead of MFMAs (the A/B knob)
+    bool ws_parts = true;  // the buffers hold part records and kXcds part-groups' records
 };
 
 // The device buffers of one launch (one layer): the cache slabs of sequence
@@ -182,6 +185,8 @@ struct LaunchBuffers {
     float *ws_o;
     float2 *ws_ml;
     int *counters;
+    float *ws_po;    // spread launches: kXcds part records of G heads x head_dim
+    float2 *ws_pml;  // and their (max, sum)
 };
 
 LaunchShape shape_of(const leap_hip_attention *h)
@@ -232,6 +237,31 @@ int max_chunks_for(int seq_len, int head_dim, int group, int cap)
     return std::max(1, std::min(cap, (seq_len + quantum - 1) / quantum));
 }
 
+using MergeFn = void (*)(leap::StepArgs);
+
+MergeFn pick_merge(int hd, int g)
+{
+#define LEAP_CASE(HD, G) \
+    if (hd == HD && g == G) return leap::part_merge_kernel<HD, G>;
+    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+#undef LEAP_CASE
+    return nullptr;
+}
+
+// A launch of fewer (sequence, KV head) groups than XCDs leaves XCDs idle
+// (a group's chunks share one L2).  When the groups stream at least
+// kSpreadBytes of K/V rows each, each group's chunks are cut into 2, 4 or 8
+// parts, one per XCD, and a second, small launch merges the parts' records
+// across the L2s.  One CU takes in about 30-40 GB/s, so a group's 32 CUs
+// stream 4 MiB in about 3-4 us, and the merge launch costs about 2 us:
+// below that size the launch on fewer XCDs is faster (measured at 1, 2 and
+// 4 KV heads, contexts 512-4096).
+#ifndef LEAP_SPREAD_MIN_BYTES
+#define LEAP_SPREAD_MIN_BYTES (4ll << 20)
+#endif
+constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
+
 // Enqueue one decode-attention launch.  Returns 0, or a HIP error code
 // (hipErrorInvalidValue for a shape without a kernel or a launch too large).
 hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_seq, const int *pos_dev,
@@ -242,8 +272,13 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     KernelFn fn = pick_kernel(hd, s.group, kind, s.valu);
     if (!fn) return hipErrorInvalidValue;
     const int chunk = choose_chunk(s, n_seq, total_rows, max_pos + 1);
-    const int grid_x = (max_pos + 1 + chunk - 1) / chunk;
-    if (grid_x > s.max_chunks) return hipErrorInvalidValue;
+    const int n_chunk_max = (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
+    if (n_chunk_max > s.max_chunks) return hipErrorInvalidValue;
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
+    int spread_log2 = 0;
+    if (kind == kDecode && s.ws_parts && total_rows * s.n_kv_heads * s.head_dim * 8ll >= n_groups * kSpreadBytes)
+        while (n_groups << (spread_log2 + 1) <= leap::kXcds && n_chunk_max >= (2 << spread_log2)) spread_log2++;
+    const int grid_x = (n_chunk_max + (1 << spread_log2) - 1) >> spread_log2;  // chunks per part
 
     leap::StepArgs a{};
     a.q = q;
@@ -268,16 +303,25 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     a.n_groups = n_seq * s.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
 
-    // Workgroup id = ((group / 8) * grid_x + chunk) * 8 + group % 8, with
-    // group = seq * n_kv_heads + kv_head: a group's chunks share one XCD.
-    const long long n_groups = (long long)n_seq * s.n_kv_heads;
-    const long long n_wg = (n_groups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
+    a.spread_log2 = spread_log2;
+    a.ws_po = b.ws_po;
+    a.ws_pml = b.ws_pml;
+
+    // Workgroup id = ((pg / 8) * grid_x + chunk) * 8 + pg % 8, with the
+    // part-group pg = (seq * n_kv_heads + kv_head) * 2^spread_log2 + part:
+    // a part-group's chunks share one XCD.
+    const long long n_pgroups = n_groups << spread_log2;
+    const long long n_wg = (n_pgroups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
     if (n_wg > 0x7fffffffLL) return hipErrorInvalidValue;
     // One pass per workgroup and at least two workgroups per CU: a CU's
     // second workgroup receives its rows after its first, so each group's
     // first-dispatched half of chunks can fold while the rest streams.
-    a.merge_asym = (chunk == leap::rows_per_pass(hd, s.group, kWaves) && n_groups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
-    return launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
+    a.merge_asym = (chunk == leap::rows_per_pass(hd, s.group, kWaves) && n_pgroups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
+    hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
+    if (e != hipSuccess || spread_log2 == 0) return e;
+    MergeFn mf = pick_merge(hd, s.group);
+    if (!mf) return hipErrorInvalidValue;
+    return launch_k(mf, dim3((unsigned)n_groups), dim3((unsigned)(s.group * hd / 4)), stream, a);
 }
 
 int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int pos_scalar,
@@ -288,7 +332,7 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
         return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", h->cfg.head_dim, h->group);
     const size_t loff = (size_t)(layer - h->cfg.layer_begin) * h->layer_floats;
     const LaunchBuffers b{h->k_cache + loff, h->v_cache + loff, (long long)h->slab_floats, h->rope,
-                          h->ws_o,           h->ws_ml,          h->counters};
+                          h->ws_o,           h->ws_ml,          h->counters,          h->ws_po, h->ws_pml};
     HIP_TRY(h, launch_attention(shape_of(h), b, n_seq, pos_dev, pos_scalar, max_pos, total_rows, q, k, v, out,
                                 stream, kind));
     return 0;
@@ -601,10 +645,15 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
                               hipMemcpyHostToDevice, h->stream));
 
     h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, h->group, leap::kMaxChunks);
-    const size_t ws_rows = (size_t)c.max_batch * c.n_heads * leap::records_per_head(h->max_chunks);
+    // records and counters for max_batch * n_kv_heads groups, or for kXcds
+    // part-groups when a launch spreads fewer groups over the XCDs
+    const size_t n_pg = std::max<size_t>((size_t)c.max_batch * c.n_kv_heads, leap::kXcds);
+    const size_t ws_rows = n_pg * h->group * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    h->counter_bytes = (size_t)c.max_batch * c.n_kv_heads * leap::counters_per_group(h->max_chunks) * sizeof(int);
+    h->counter_bytes = n_pg * leap::counters_per_group(h->max_chunks) * sizeof(int);
+    CREATE_TRY(hipMalloc(&h->ws_po, (size_t)leap::kXcds * h->group * c.head_dim * sizeof(float)));
+    CREATE_TRY(hipMalloc(&h->ws_pml, (size_t)leap::kXcds * h->group * sizeof(float2)));
     CREATE_TRY(hipMalloc(&h->counters, h->counter_bytes));
     CREATE_TRY(hipMemsetAsync(h->counters, 0, h->counter_bytes, h->stream));
     // rounded up to 16 bytes: the inputs are staged in as 16-byte words
@@ -627,7 +676,8 @@ int leap_hip_attention_destroy(leap_hip_attention *h)
     if (!h) return 0;
     (void)hipSetDevice(h->cfg.device);  // the handle's device, as for every other call
     if (h->stream) (void)hipStreamSynchronize(h->stream);
-    void *bufs[] = {h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->in_dev,
+    void *bufs[] = {h->ws_po,   h->ws_pml,
+                    h->k_cache, h->v_cache, h->rope,  h->ws_o,  h->ws_ml, h->counters, h->in_dev,
                     h->out_dev, h->blk,     h->w_qkv, h->w_o,   h->w_rms, h->w8_qkv,   h->s8_qkv,
                     h->w8_o,    h->s8_o,    h->q8_act, h->q8_act_s};
     for (void *p : bufs)
@@ -681,9 +731,13 @@ constexpr int kScratchDevices = 64;
 constexpr int kScratchMaxKvHeads = 128;
 // The arrival counters sit at the start of the array, in a region of the
 // same size for every shape: the records of one shape must never overlap
-// the counters of another, which have to stay zero between calls.
+// the counters of another, which have to stay zero between calls.  Then the
+// part records of spread launches (kXcds part-groups of up to 8 heads of
+// 128), then a shape's chunk records.
 constexpr size_t kScratchCounterBytes =
     (size_t)kScratchMaxKvHeads * leap::counters_per_group(kScratchChunks) * sizeof(int);
+constexpr size_t kScratchPartOBytes = (size_t)leap::kXcds * 8 * 128 * sizeof(float);
+constexpr size_t kScratchPartMlBytes = (size_t)leap::kXcds * 8 * sizeof(float2);
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -702,8 +756,10 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 // (max, sum) records, then its partial outputs, each 256-byte aligned.
 void scratch_layout(const leap_hip_attention_config &c, size_t *ml_off, size_t *o_off, size_t *total)
 {
-    const size_t rec = (size_t)c.n_heads * leap::records_per_head(kScratchChunks);
-    *ml_off = align256(kScratchCounterBytes);
+    // records for n_kv_heads groups, or for kXcds part-groups of a spread launch
+    const size_t n_pg = std::max<size_t>((size_t)c.n_kv_heads, leap::kXcds);
+    const size_t rec = n_pg * (size_t)(c.n_heads / c.n_kv_heads) * leap::records_per_head(kScratchChunks);
+    *ml_off = align256(kScratchCounterBytes) + align256(kScratchPartOBytes) + align256(kScratchPartMlBytes);
     *o_off = *ml_off + align256(rec * sizeof(float2));
     *total = *o_off + rec * (size_t)c.head_dim * sizeof(float);
 }
@@ -777,13 +833,16 @@ int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int po
     });
     if (d.rc) return set_err(nullptr, d.rc, "%s", d.msg);
     const LaunchShape shape{c.head_dim, group, c.n_heads, c.n_kv_heads, c.seq_len, d.n_cu, 0, kScratchChunks};
+    const size_t po_off = align256(kScratchCounterBytes), pml_off = po_off + align256(kScratchPartOBytes);
     const LaunchBuffers b{k_cache,
                           v_cache,
                           0,
                           reinterpret_cast<const float4 *>(rope),
                           reinterpret_cast<float *>(d.ptr + o_off),
                           reinterpret_cast<float2 *>(d.ptr + ml_off),
-                          reinterpret_cast<int *>(d.ptr)};
+                          reinterpret_cast<int *>(d.ptr),
+                          reinterpret_cast<float *>(d.ptr + po_off),
+                          reinterpret_cast<float2 *>(d.ptr + pml_off)};
     const hipError_t e = launch_attention(shape, b, 1, nullptr, pos, pos, pos + 1, q, k_new, v_new, out,
                                           (hipStream_t)stream);
     if (e != hipSuccess) {

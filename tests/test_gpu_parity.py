@@ -343,3 +343,54 @@ def test_random_shapes_positions_and_batches(nh, nkv, hd, T, split, batch):
         out = att.step(0, int(pos[0]), q[0], k[0], v[0])[None] if batch == 1 else att.step_batched(0, pos, q, k, v)
         for i in range(batch):
             _step_and_check(att, 0, int(pos[i]), q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+# ---- few KV heads: a group's chunks spread over several XCDs ------------------------
+
+@pytest.mark.parametrize("nh,nkv,hd,T,split", [
+    (8, 1, 128, 4096, 0),     # one group over eight XCDs (4 MiB of K/V rows)
+    (16, 2, 128, 4096, 0),    # two groups, four parts each
+    (32, 4, 64, 8192, 0),     # TinyLlama heads at a long context, two parts each
+    (32, 4, 128, 8000, 0),
+    (8, 1, 64, 20000, 0),
+    (8, 1, 128, 4096, 256),   # forced chunking: 16 chunks, eight parts of two
+    (24, 3, 128, 9000, 0),    # three groups, two parts each (six XCDs)
+    (32, 4, 64, 2048, 0),     # 2 MiB per group: no spread (the faster launch there)
+    (32, 8, 128, 4096, 0),    # eight groups: no spread
+])
+def test_spread_over_xcds_few_kv_heads(nh, nkv, hd, T, split):
+    theta = 500000.0
+    rng = rng_for(nh, nkv, hd, T, split, 7)
+    with HipAttention(nh, nkv, hd, T + 3, rope_theta=theta) as att:
+        if split:
+            att.set_split(split)
+        pos = T - 1
+        att.kv_upload(0, 0, 0, normal(rng, (pos, nkv * hd), hd), normal(rng, (pos, nkv * hd), hd))
+        for rep in range(2):  # twice: the second launch finds the workspace as the first left it
+            q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+            out = att.step(0, pos, q, k, v)
+            _step_and_check(att, 0, pos, q, k, v, theta, out=out)
+
+
+def test_spread_ragged_batch_with_empty_parts():
+    """Two sequences of two KV heads (four groups, two parts each) at very
+    different positions: the short one's second part has no chunks."""
+    nh, nkv, hd = 16, 2, 128
+    Ts = [9000, 100]
+    rng = rng_for(8, 8)
+    with HipAttention(nh, nkv, hd, 9003, max_batch=2) as att:
+        rows = []
+        for s, T in enumerate(Ts):
+            kr, vr = normal(rng, (T - 1, nkv * hd), hd), normal(rng, (T - 1, nkv * hd), hd)
+            att.kv_upload(s, 0, 0, kr, vr)
+            rows.append((kr, vr))
+        q = normal(rng, (2, nh * hd), hd)
+        k, v = normal(rng, (2, nkv * hd), hd), normal(rng, (2, nkv * hd), hd)
+        out = att.step_batched(0, [T - 1 for T in Ts], q, k, v)
+        for s, T in enumerate(Ts):
+            orc = O.Oracle(1, nh, nkv, hd, 9003)
+            orc.key_cache[0, :T - 1], orc.value_cache[0, :T - 1] = rows[s]
+            want, _ = orc.step(0, T - 1, q[s], k[s], v[s])
+            assert_close(out[s], want, what=f"sequence {s}")
+            kr, vr = att.kv_download(s, 0, T - 1, T)
+            assert np.array_equal(kr[0], orc.key_cache[0, T - 1]) and np.array_equal(vr[0], orc.value_cache[0, T - 1])

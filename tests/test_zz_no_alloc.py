@@ -96,7 +96,7 @@ def test_noalloc_alternating_shapes_share_the_workspace():
     import torch
     dev = torch.device("cuda:0")
     shapes = [(64, 8, 128, 8192, 500000.0), (32, 4, 64, 512, 10000.0), (32, 8, 128, 4096, 500000.0),
-              (8, 2, 128, 2048, 500000.0)]
+              (8, 2, 128, 2048, 500000.0), (8, 1, 128, 4096, 500000.0)]  # the last spreads over 8 XCDs
     atts, ropes, caches = [], [], []
     try:
         for i, (nh, nkv, hd, sl, th) in enumerate(shapes):
