@@ -331,10 +331,11 @@ class Workload:
         launch alone, kind 2: the bare K/V stream) with this step's shape."""
         att, sp, L = self.att, self.stream.cuda_stream, self.L
         n, mp, tr = self.batch, self.max_pos, (self.total_rows if self.batch > 1 else self.max_pos + 1)
+        pp = self.pos_dev.data_ptr() if self.batch > 1 else None
 
         def one():
             for l in range(L):
-                att.floor_async(kind, l, n, mp, tr, sp)
+                att.floor_async(kind, l, n, mp, tr, sp, pos_ptr=pp)
         ms, _, _ = timed_steps(one, self.stream, steps, warmup, L)
         return ms * 1e3 / (steps * L)
 

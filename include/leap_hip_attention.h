@@ -334,14 +334,16 @@ int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention
 /* Measurement floors of a step's launch shape (no counterpart in the
  * reference): enqueue on `stream` one launch with the grid, block size and
  * argument block that leap_hip_attention_step_batched_async(h, layer,
- * n_seq, pos = max_pos for every sequence, max_pos, total_rows, ...) would
- * make, running kind 1: a kernel that reads its arguments and exits (the
- * launch floor), or kind 2: a kernel that streams the same K and V rows with
- * the same loads and only sums them (the launch plus bare-stream floor).
- * Neither writes memory nor changes the cache.  n_seq = 1, max_pos = pos,
- * total_rows = pos + 1 is the single-sequence step. */
-int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, int max_pos,
-                                   long long total_rows, void *stream);
+ * n_seq, pos, max_pos, total_rows, ...) would make, running kind 1: a
+ * kernel that reads its arguments and exits (the launch floor), or kind 2:
+ * a kernel that streams the same K and V rows ([0, pos[i]] of each
+ * sequence) with the same loads and only sums them (the launch plus
+ * bare-stream floor).  pos is device memory as in step_batched_async, or
+ * NULL for every sequence at max_pos.  Neither kind writes memory or
+ * changes the cache.  n_seq = 1, pos = NULL, max_pos = the position,
+ * total_rows = position + 1 is the single-sequence step. */
+int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, const int *pos,
+                                   int max_pos, long long total_rows, void *stream);
 
 /* Placement diagnostic: launch n_wg workgroups of the decode kernel's size on
  * `device` and write the XCD (XCC_ID) each ran on to xcc_out[n_wg].  The

@@ -113,7 +113,7 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_packet_upload.argtypes = [H, ctypes.c_char_p, ctypes.c_size_t, _P, _IP, _IP, _P]
     L.leap_hip_attention_packet_download.argtypes = [H, _P, _I, _I, _P, ctypes.c_size_t, _P]
     L.leap_hip_attention_xcc_map.argtypes = [_I, _I, ctypes.POINTER(_I)]
-    L.leap_hip_attention_floor_async.argtypes = [H, _I, _I, _I, _I, ctypes.c_longlong, _P]
+    L.leap_hip_attention_floor_async.argtypes = [H, _I, _I, _I, _P, _I, ctypes.c_longlong, _P]
     L.leap_hip_attention_set_products.argtypes = [H, _I]
     L.leap_hip_attention_step_noalloc.argtypes = [ctypes.POINTER(Config), _I] + [_P] * 8
     for name in EXPORTS:
@@ -343,10 +343,13 @@ class HipAttention:
                                                               _fp(c), _fp(s)))
         return c, s
 
-    def floor_async(self, kind, layer, n_seq, max_pos, total_rows, stream=0):
+    def floor_async(self, kind, layer, n_seq, max_pos, total_rows, stream=0, pos_ptr=None):
         """Enqueue a floor launch of a step's shape: kind 1 launch only,
-        kind 2 the bare K/V stream (measurement; writes nothing)."""
-        self._check(self.lib.leap_hip_attention_floor_async(self.h, kind, layer, n_seq, max_pos, total_rows, stream))
+        kind 2 the bare K/V stream (measurement; writes nothing).  pos_ptr:
+        device address of the n_seq positions, or None for every sequence
+        at max_pos."""
+        self._check(self.lib.leap_hip_attention_floor_async(self.h, kind, layer, n_seq, pos_ptr, max_pos,
+                                                            total_rows, stream))
 
     def set_products(self, valu: bool):
         """Score and weighted-V products on the VALU (True) or the matrix cores."""

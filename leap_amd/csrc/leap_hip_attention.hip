@@ -1236,8 +1236,8 @@ int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int p
     return 0;
 }
 
-int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, int max_pos,
-                                   long long total_rows, void *stream)
+int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, const int *pos,
+                                   int max_pos, long long total_rows, void *stream)
 {
     if (!h) return -EINVAL;
     if (kind != kFloorLaunch && kind != kFloorStream) return set_err(h, -EINVAL, "floor kind %d is not 1 or 2", kind);
@@ -1248,9 +1248,10 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
         return set_err(h, -EINVAL, "max_pos %d outside [0, %d)", max_pos, h->cfg.seq_len);
     if (total_rows <= 0 || total_rows > (long long)n_seq * (max_pos + 1))
         return set_err(h, -EINVAL, "total_rows %lld outside [1, %lld]", total_rows, (long long)n_seq * (max_pos + 1));
+    if (reinterpret_cast<uintptr_t>(pos) % 4) return set_err(h, -EINVAL, "pos must be 4-byte aligned");
     HIP_TRY(h, hipSetDevice(h->cfg.device));
-    // every sequence at max_pos (the kernels read no positions array)
-    return launch(h, layer, n_seq, nullptr, max_pos, max_pos, total_rows, nullptr, nullptr, nullptr, h->out_dev,
+    // with pos NULL, every sequence at max_pos
+    return launch(h, layer, n_seq, pos, max_pos, max_pos, total_rows, nullptr, nullptr, nullptr, h->out_dev,
                   (hipStream_t)stream, kind);
 }
 

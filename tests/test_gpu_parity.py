@@ -228,18 +228,21 @@ def test_batched_small_ragged_with_tiny_contexts():
 
 
 def test_llama3_70b_stage_batch16_ctx8192():
-    """64/8/128, batch 16, T = 8192, one of the stage's 20 layers."""
+    """64/8/128, batch 16, T = 8192: a handle holding the whole 20-layer
+    stage [20, 40) of the 80-layer model; the first and the last held layer
+    are stepped and every sequence is checked on both."""
     nh, nkv, hd, S, T = 64, 8, 128, 16, 8192
     rng = rng_for(5, S)
-    with HipAttention(nh, nkv, hd, T, n_layers=80, layer_begin=20, layer_end=21,
+    with HipAttention(nh, nkv, hd, T, n_layers=80, layer_begin=20, layer_end=40,
                       max_batch=S) as att:
         att.kv_fill_normal(0x4C454150 + 3, 1.0 / np.sqrt(hd))
-        q = normal(rng, (S, nh * hd), hd)
-        k = normal(rng, (S, nkv * hd), hd)
-        v = normal(rng, (S, nkv * hd), hd)
-        out = att.step_batched(20, np.full(S, T - 1), q, k, v)
-        for i in (0, 7, 15):
-            _step_and_check(att, 20, T - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+        for layer in (20, 39):
+            q = normal(rng, (S, nh * hd), hd)
+            k = normal(rng, (S, nkv * hd), hd)
+            v = normal(rng, (S, nkv * hd), hd)
+            out = att.step_batched(layer, np.full(S, T - 1), q, k, v)
+            for i in range(S):
+                _step_and_check(att, layer, T - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
 
 
 # ---- cache management and errors ----------------------------------------------------

@@ -107,6 +107,8 @@ def test_floor_launches_write_nothing(kind):
         s = torch.cuda.Stream()
         att.floor_async(kind, 1, 1, T - 1, T, s.cuda_stream)
         att.floor_async(kind, 1, 3, 1000, 3 * 1001, s.cuda_stream)
+        pos = torch.tensor([1000, 17, T - 1], dtype=torch.int32, device="cuda:0")
+        att.floor_async(kind, 1, 3, T - 1, 1001 + 18 + T, s.cuda_stream, pos_ptr=pos.data_ptr())
         s.synchronize()
         k1, v1 = att.kv_download(2, 1, 0, T)
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
@@ -114,3 +116,5 @@ def test_floor_launches_write_nothing(kind):
             att.floor_async(3, 1, 1, T - 1, T, s.cuda_stream)
         with pytest.raises(LeapError):
             att.floor_async(kind, 1, 4, T - 1, T, s.cuda_stream)
+        with pytest.raises(LeapError):  # positions not 4-byte aligned
+            att.floor_async(kind, 1, 1, T - 1, T, s.cuda_stream, pos_ptr=pos.data_ptr() + 2)
