@@ -301,7 +301,8 @@ int leap_hip_attention_rope_download(leap_hip_attention *h, int pos_begin, int p
                                      float *cos_out, float *sin_out);
 
 /* Positions per split-K chunk for later steps: 0 restores the automatic
- * choice; otherwise a multiple of 64.  A tuning and test knob. */
+ * choice; otherwise a multiple of 8 (a chunk that is not a whole number of
+ * 64-row passes masks the rows past its end).  A tuning and test knob. */
 int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions);
 
 /* Where later steps compute the score (q . K) and weighted-V products: 0 on

@@ -99,7 +99,7 @@ struct StepArgs {
     int seq_len;
     int n_heads;
     int n_kv_heads;
-    int chunk;           // positions per workgroup, multiple of rows_per_pass(HD, G, NW)
+    int chunk;           // positions per workgroup, a multiple of 8 (passes past its end are masked)
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
@@ -107,9 +107,30 @@ struct StepArgs {
                          // first-dispatched half of a group's chunks finishes first
     int spread_log2;     // a group's chunks are cut into 2^spread_log2 parts on as many
                          // XCDs (launches of fewer groups than XCDs); 0: one part
+    int even_chunks;     // > 0: a sequence of T positions is cut instead into min(even_chunks, T)
+                         // chunks of near-equal length (seq_chunks, chunk_start); in the
+                         // slot before the 8-byte aligned pointers, so that the fields the
+                         // prologue reads first keep their offsets
     float *ws_po;        // [n_groups << spread_log2][G][HD] each part's unnormalised output
     float2 *ws_pml;      // [n_groups << spread_log2][G] its (max, sum), log2 units
 };
+
+// Chunks of a sequence of T positions, and where chunk c starts: fixed-size
+// chunks of a.chunk rows (the last one shorter), or min(even_chunks, T)
+// chunks of near-equal length, the first T mod n of them one row longer
+// (one 32-bit quotient per sequence, ahead of the first loads).
+__device__ __forceinline__ int seq_chunks(const StepArgs &a, int T)
+{
+    return a.even_chunks > 0 ? min(a.even_chunks, T) : (T + a.chunk - 1) / a.chunk;
+}
+__device__ __forceinline__ int chunk_start(const StepArgs &a, int T, int n_chunks, int c)
+{
+    if (a.even_chunks > 0) {
+        const unsigned q = (unsigned)T / (unsigned)n_chunks, r = (unsigned)T - q * (unsigned)n_chunks;
+        return (int)((unsigned)c * q + min((unsigned)c, r));
+    }
+    return min(c * a.chunk, T);
+}
 
 // ---- buffer access ------------------------------------------------------------
 //
@@ -289,7 +310,13 @@ struct Shape {
 // MFMA: the score and weighted-V products on the matrix cores (4x4x1 f32
 // MFMAs); false: the same products as per-lane VALU FMAs, leaving the same
 // partial sums in the same lanes (the A/B of the matrix-core choice).
-template <int HD, int G, int NW, bool MFMA = true>
+// PART: chunks that need not be whole passes (near-equal chunks, or forced
+// sizes that are multiples of 8): rows past a chunk's end are masked, and
+// only the chunk holding pos writes the new token.  Launches of whole-pass
+// fixed-size chunks use PART = false, whose prologue is shorter (the two
+// measured 0.07-0.14 us apart per launch at Llama-3-8B ctx 4096 and
+// TinyLlama ctx 256).
+template <int HD, int G, int NW, bool MFMA = true, bool PART = false>
 __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
@@ -317,7 +344,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
     const int T = pos + 1;
-    const int n_chunks = (T + a.chunk - 1) / a.chunk;
+    const int n_chunks = PART ? seq_chunks(a, T) : (T + a.chunk - 1) / a.chunk;
     if (chunk_id >= n_chunks) return;
     // chunks of this part (at least 1 here)
     const int n_local = min(a.grid_chunks, n_chunks - part * a.grid_chunks);
@@ -328,9 +355,24 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const size_t slab = (size_t)seq * (size_t)a.seq_stride;
     float *kc = a.k_cache + slab + (size_t)kvh * HD;
     float *vc = a.v_cache + slab + (size_t)kvh * HD;
-    // Rows [0, pos) of this KV head are in range; row pos and beyond read 0.
-    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc, (uint32_t)pos * row_bytes);
-    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)pos * row_bytes);
+    // This chunk's rows [chunk_begin, last].  With PART a pass may reach past
+    // the chunk's end.  Rows up to min(pos, chunk end) of this KV head are in
+    // range: row pos (the new token, from registers) and the rows beyond
+    // read 0 without touching memory, and their scores are masked.
+    int chunk_begin, chunk_end, row_end, last;
+    if constexpr (PART) {
+        chunk_begin = chunk_start(a, T, n_chunks, chunk_id);
+        chunk_end = chunk_start(a, T, n_chunks, chunk_id + 1);
+        row_end = min(pos, chunk_end);
+        last = min(pos, chunk_end - 1);
+    } else {
+        chunk_begin = chunk_id * a.chunk;
+        chunk_end = min(chunk_begin + a.chunk, T);
+        row_end = pos;
+        last = pos;
+    }
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc, (uint32_t)row_end * row_bytes);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)row_end * row_bytes);
     const float *k_row_new = a.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
     const float *v_row_new = a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
     const float *qg = a.q + (size_t)seq * q_dim + (size_t)kvh * G * HD;
@@ -360,9 +402,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     // per thread) ahead of the first K/V tile, rotated with the score scale
     // folded in, and shared through LDS; only the workgroup whose chunk holds
     // pos loads and rotates the new token's k and v.
-    const int chunk_begin = chunk_id * a.chunk;
     // passes over this chunk's rows that reach a position <= pos
-    const int n_sub = (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
+    const int n_sub = PART ? (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS
+                           : (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
     const bool has_pos = (chunk_id == n_chunks - 1);
     constexpr int PAIRS = G * HD / 2;
     constexpr int QP = (PAIRS + S::THREADS - 1) / S::THREADS;  // q pairs per thread
@@ -476,7 +518,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const int t = base + ks * 8 + krow;
-            if (t == pos) {
+            if ((!PART || has_pos) && t == pos) {
 #pragma unroll
                 for (int f = 0; f < NF; f++) {
                     kb[ks][f] = rope4(knew[f], tab[f]);
@@ -490,7 +532,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         float s[KS][G];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const bool ok = score_lane && (base + ks * 8 + krow <= pos);
+            const bool ok = score_lane && (base + ks * 8 + krow <= last);
 #pragma unroll
             for (int qd = 0; qd < GQ; qd++) {
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -579,7 +621,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const int r = vs * RPV + vg;
-            if (base + r == pos) {
+            if ((!PART || has_pos) && base + r == pos) {
                 vb[vs] = vnew;
                 *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
             }
@@ -944,7 +986,7 @@ __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
     const int seq = group / a.n_kv_heads, kvh = group % a.n_kv_heads;
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
-    const int n_chunks = (pos + 1 + a.chunk - 1) / a.chunk;
+    const int n_chunks = seq_chunks(a, pos + 1);
     const int n_parts = min(1 << a.spread_log2, (n_chunks + a.grid_chunks - 1) / a.grid_chunks);
     const int h = threadIdx.x / D4, c = threadIdx.x % D4;
     const size_t pg0 = (size_t)group << a.spread_log2;
@@ -996,17 +1038,19 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
     const int T = pos + 1;
-    const int n_chunks = (T + a.chunk - 1) / a.chunk;
+    const int n_chunks = seq_chunks(a, T);
     if (chunk_id >= n_chunks) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const uint32_t row_bytes = (uint32_t)(a.n_kv_heads * HD) * 4u;
     const size_t slab = (size_t)seq * (size_t)a.seq_stride;
-    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k_cache + slab + (size_t)kvh * HD, (uint32_t)pos * row_bytes);
-    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v_cache + slab + (size_t)kvh * HD, (uint32_t)pos * row_bytes);
+    const int chunk_begin = chunk_start(a, T, n_chunks, chunk_id);
+    const int chunk_end = chunk_start(a, T, n_chunks, chunk_id + 1);
+    const uint32_t range = (uint32_t)min(pos, chunk_end) * row_bytes;  // as the step's
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k_cache + slab + (size_t)kvh * HD, range);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v_cache + slab + (size_t)kvh * HD, range);
     const int kj = lane & 3, ksl = (lane >> 2) & 7, kq = lane >> 5, krow = 4 * kq + kj;
     const int vg = lane / LPV, vj = lane % LPV;
-    const int chunk_begin = chunk_id * a.chunk;
-    const int n_sub = (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
+    const int n_sub = (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS;
     float sum = 0.0f;
     for (int sub = 0; sub < n_sub; sub++) {
         const int base = chunk_begin + (sub * NW + wave) * R;

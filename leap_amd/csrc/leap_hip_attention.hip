@@ -138,14 +138,18 @@ constexpr int kThreads = kWaves * leap::kWave;
 // grid (measurement only).
 enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
 
-KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false)
+// part: chunks that are not all whole passes (near-equal chunks, or a forced
+// size that is not a multiple of a pass).
+KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false, bool part = false)
 {
-#define LEAP_CASE(HD, G)                                                                  \
-    if (hd == HD && g == G)                                                               \
-        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>          \
-               : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>          \
-               : valu                 ? leap::decode_attention_kernel<HD, G, kWaves, false> \
-                                      : leap::decode_attention_kernel<HD, G, kWaves, true>;
+#define LEAP_CASE(HD, G)                                                                                   \
+    if (hd == HD && g == G)                                                                                \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>                           \
+               : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>                           \
+               : part ? (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, true>                  \
+                              : leap::decode_attention_kernel<HD, G, kWaves, true, true>)                  \
+                      : (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, false>                 \
+                              : leap::decode_attention_kernel<HD, G, kWaves, true, false>);
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
@@ -206,15 +210,24 @@ LaunchShape shape_of(const leap_hip_attention *h)
 // The sequence length (the mean one when ragged) is cut into equal chunks,
 // rounded up to whole passes; at most s.max_chunks chunks per sequence.
 constexpr long long kLatencyBytes = 128ll << 20;
+#ifndef LEAP_CHUNK_ROWS
+#define LEAP_CHUNK_ROWS 64
+#endif
+#ifndef LEAP_MIN_CHUNK
+#define LEAP_MIN_CHUNK 64
+#endif
+constexpr int kChunkRows = LEAP_CHUNK_ROWS;  // granularity of the automatic chunk sizes
+constexpr int kMinChunk = LEAP_MIN_CHUNK;    // smallest automatic chunk
+constexpr int kSplitRows = 8;                // granularity of any chunk (one MFMA row set)
 
 int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
     const int quantum = leap::rows_per_pass(s.head_dim, s.group, kWaves);
-    const int floor_chunk = round_up((max_T + s.max_chunks - 1) / s.max_chunks, quantum);
+    const int floor_chunk = round_up((max_T + s.max_chunks - 1) / s.max_chunks, kSplitRows);
     const long long kv_dim = (long long)s.n_kv_heads * s.head_dim;
     int c;
     if (s.split > 0) {
-        c = round_up(s.split, quantum);
+        c = round_up(s.split, kSplitRows);
     } else {
         const long long bytes = total_rows * kv_dim * 8ll;
         const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
@@ -223,18 +236,52 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         const long long want_wgs = std::max<long long>(1, per_cu * s.n_cu);
         const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
         const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
-        c = round_up((int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20), quantum);
+        c = (int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20);
+        c = c > quantum ? round_up(c, quantum) : std::max(kMinChunk, round_up(c, kChunkRows));
+        c = std::min(c, round_up(max_T, quantum));
     }
-    c = std::min(c, round_up(max_T, quantum));
-    return std::max(c, std::max(floor_chunk, quantum));
+    return std::max(c, std::max(floor_chunk, kSplitRows));
+}
+
+// The latency regime's split of equal-length sequences into exactly per_seq
+// chunks of near-equal length (0: use choose_chunk), when each chunk is then
+// one pass of more than kEvenMinRows rows.  Fixed 64-row chunks leave
+// ceil(T / 64) chunks per sequence, and for most contexts that is not a
+// whole number of workgroups per CU: past 2048 positions at Llama-3-8B,
+// 288-480 workgroups on 256 CUs put a second chunk on some CUs only, and
+// those finish late (10.4-10.8 us at ctx 2304-3584 against 8.1 at 2048).
+// The even split keeps two one-pass workgroups on every CU and the
+// asymmetric merge (9.1-9.9 us).  Shorter chunks than kEvenMinRows were
+// slower than 64-row chunks on fewer CUs (ctx 2048: 8.7 against 8.1 us).
+constexpr int kEvenMinRows = 32;
+
+int even_chunks_for(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
+{
+    if (s.split > 0) return 0;
+    const int pass = leap::rows_per_pass(s.head_dim, s.group, kWaves);
+    const long long bytes = total_rows * (long long)s.n_kv_heads * s.head_dim * 8ll;
+    const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
+    if (bytes > kLatencyBytes || ragged) return 0;
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
+    const long long per_seq = std::max<long long>(1, (2ll * s.n_cu + n_groups / 2) / n_groups);
+    if (per_seq < 2 || per_seq > s.max_chunks) return 0;
+    // exactly one pass per chunk: fixed-size chunks cut the same rows
+    if (max_T <= kEvenMinRows * per_seq || max_T >= pass * per_seq) return 0;
+    return (int)per_seq;
 }
 
 // Most chunks per sequence any launch of a handle can make, for sizing its
-// workspace: every chunk is at least one pass of rows.
-int max_chunks_for(int seq_len, int head_dim, int group, int cap)
+// workspace: a pass of rows per chunk; the even split of one sequence
+// (even_chunks_for: up to 2 * n_cu / n_kv_heads chunks of more than
+// kEvenMinRows rows); forced splits down to kSplitRows rows, up to 64
+// chunks.
+int max_chunks_for(int seq_len, int head_dim, int group, int n_kv_heads, int n_cu, int cap)
 {
     const int quantum = leap::rows_per_pass(head_dim, group, kWaves);
-    return std::max(1, std::min(cap, (seq_len + quantum - 1) / quantum));
+    const int by_pass = (seq_len + quantum - 1) / quantum;
+    const int even = std::min((2 * n_cu + n_kv_heads / 2) / n_kv_heads, seq_len / kEvenMinRows);
+    const int by_rows = std::min(64, (seq_len + kSplitRows - 1) / kSplitRows);
+    return std::max(1, std::min(cap, std::max(by_pass, std::max(even, by_rows))));
 }
 
 using MergeFn = void (*)(leap::StepArgs);
@@ -269,10 +316,12 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
                             const float *v, float *out, hipStream_t stream, int kind = kDecode)
 {
     const int hd = s.head_dim;
-    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu);
+    const int even = even_chunks_for(s, n_seq, total_rows, max_pos + 1);
+    const int chunk = even ? (max_pos + even) / even : choose_chunk(s, n_seq, total_rows, max_pos + 1);
+    const bool part = even > 0 || chunk % leap::rows_per_pass(hd, s.group, kWaves) != 0;
+    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part);
     if (!fn) return hipErrorInvalidValue;
-    const int chunk = choose_chunk(s, n_seq, total_rows, max_pos + 1);
-    const int n_chunk_max = (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
+    const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
     if (n_chunk_max > s.max_chunks) return hipErrorInvalidValue;
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
     int spread_log2 = 0;
@@ -299,6 +348,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     a.n_heads = s.n_heads;
     a.n_kv_heads = s.n_kv_heads;
     a.chunk = chunk;
+    a.even_chunks = even;
     a.grid_chunks = grid_x;
     a.n_groups = n_seq * s.n_kv_heads;
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
@@ -316,7 +366,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     // One pass per workgroup and at least two workgroups per CU: a CU's
     // second workgroup receives its rows after its first, so each group's
     // first-dispatched half of chunks can fold while the rest streams.
-    a.merge_asym = (chunk == leap::rows_per_pass(hd, s.group, kWaves) && n_pgroups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
+    a.merge_asym = (chunk <= leap::rows_per_pass(hd, s.group, kWaves) && n_pgroups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
     hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
     MergeFn mf = pick_merge(hd, s.group);
@@ -644,7 +694,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMemcpyAsync(h->rope, packed.data(), packed.size() * sizeof(float),
                               hipMemcpyHostToDevice, h->stream));
 
-    h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, h->group, leap::kMaxChunks);
+    h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, h->group, c.n_kv_heads, h->n_cu, leap::kMaxChunks);
     // records and counters for max_batch * n_kv_heads groups, or for kXcds
     // part-groups when a launch spreads fewer groups over the XCDs
     const size_t n_pg = std::max<size_t>((size_t)c.max_batch * c.n_kv_heads, leap::kXcds);
@@ -1266,8 +1316,8 @@ int leap_hip_attention_set_products(leap_hip_attention *h, int valu)
 int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions)
 {
     if (!h) return -EINVAL;
-    if (chunk_positions < 0 || chunk_positions % 64 != 0)
-        return set_err(h, -EINVAL, "chunk %d is not a non-negative multiple of 64",
+    if (chunk_positions < 0 || chunk_positions % 8 != 0)
+        return set_err(h, -EINVAL, "chunk %d is not a non-negative multiple of 8",
                        chunk_positions);
     h->split = chunk_positions;
     return 0;

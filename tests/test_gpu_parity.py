@@ -84,7 +84,12 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
                                      (2049, 0), (777, 256),
                                      # 32, 48 and 64 one-pass chunks: the asymmetric merge when the
                                      # launch puts two workgroups on every CU
-                                     (2048, 64), (3072, 64), (4096, 64)])
+                                     (2048, 64), (3072, 64), (4096, 64),
+                                     # chunks that are not whole 64-row passes (rows past a chunk's
+                                     # end masked), with the asymmetric merge at 64 chunks
+                                     (3072, 48), (2048, 32), (1000, 40), (130, 8), (4000, 200),
+                                     # automatic: 64 near-equal chunks of 33-64 rows for 8 KV heads
+                                     (2500, 0), (3001, 0)])
 def test_step_shapes_and_splits(nh, nkv, hd, T, split):
     theta = 10000.0 if hd == 64 else 500000.0
     rng = rng_for(nh, nkv, hd, T, split)
@@ -212,13 +217,36 @@ def test_batched_ragged_llama3_8b():
             _step_and_check(att, 5, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
 
 
-def test_batched_small_ragged_with_tiny_contexts():
+@pytest.mark.parametrize("split", [64, 24])
+def test_batched_small_ragged_with_tiny_contexts(split):
     nh, nkv, hd, S = 16, 2, 128, 9
     Ts = np.array([1, 2, 63, 64, 65, 128, 129, 700, 1500])
     rng = rng_for(33)
     with HipAttention(nh, nkv, hd, 1600, max_batch=12) as att:
         att.kv_fill_normal(99, 0.1)
-        att.set_split(64)
+        att.set_split(split)
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(0, Ts - 1, q, k, v)
+        for i in range(S):
+            _step_and_check(att, 0, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+@pytest.mark.parametrize("nh,nkv,hd,Ts", [
+    (32, 8, 128, [1500, 1100]),          # 16 groups: 32 near-equal chunks each, asymmetric merge
+    (32, 8, 128, [500] * 7 + [5]),       # 64 groups: 8 chunks each, the short sequence 5 chunks of 1 row
+    (32, 4, 64, [6000]),                 # 4 groups: 128 near-equal chunks, two-level merge
+    (8, 1, 128, [20000]),                # one group: 512 near-equal chunks spread over the XCDs
+])
+def test_even_split_chunks(nh, nkv, hd, Ts):
+    """Launches that cut each sequence into a fixed number of near-equal
+    chunks (equal-length batches in the latency regime)."""
+    Ts = np.array(Ts)
+    S = len(Ts)
+    rng = rng_for(41, nh, nkv, hd, S)
+    with HipAttention(nh, nkv, hd, int(Ts.max()) + 3, max_batch=S) as att:
+        att.kv_fill_normal(0x4C454150 + 41, 1.0 / np.sqrt(hd))
         q = normal(rng, (S, nh * hd), hd)
         k = normal(rng, (S, nkv * hd), hd)
         v = normal(rng, (S, nkv * hd), hd)
@@ -302,7 +330,11 @@ def test_async_entry_points_on_a_torch_stream():
         att.step_batched_async(0, 2, pos.data_ptr(), T - 1, bq.data_ptr(), bk.data_ptr(),
                                bv.data_ptr(), bout.data_ptr(), s.cuda_stream)
         s.synchronize()
-        assert np.array_equal(bout[0].cpu().numpy(), ref)
+        # sized without the host's row count, this launch splits the positions
+        # differently from the single step (fixed 64-row chunks against 64
+        # near-equal ones): the same result up to fp32 summation order
+        assert_close(bout[0].cpu().numpy(), ref)
+        _step_and_check(att, 0, T - 1, q, k, v, 500000.0, seq=0, out=bout[0].cpu().numpy())
         _step_and_check(att, 0, 17, q, k, v, 500000.0, seq=1, out=bout[1].cpu().numpy())
         # the host's row count only changes how the positions are split
         hint = torch.empty_like(bout)
