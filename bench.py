@@ -114,7 +114,7 @@ DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
 # the configurations timed beside the headline in the default run
 EXTRA_WORKLOADS = ("tinyllama-ctx256", "llama3-8b-batch64-ragged", "llama3-70b-stage20-batch16",
                    "llama3.1-8b-ctx131072")
-SWEEP_T = (1, 16, 64, 256, 1024, 2048, 4096)
+SWEEP_T = (1, 16, 64, 256, 512, 1024, 2048, 2304, 3072, 4096)
 SWEEP_SHAPES = {"llama3-8b": (32, 32, 8, 128, 500000.0), "tinyllama": (22, 32, 4, 64, 10000.0)}
 
 
