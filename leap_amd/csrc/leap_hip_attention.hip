@@ -244,15 +244,17 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
 }
 
 // The latency regime's split of equal-length sequences into exactly per_seq
-// chunks of near-equal length (0: use choose_chunk), when each chunk is then
-// one pass of more than kEvenMinRows rows.  Fixed 64-row chunks leave
-// ceil(T / 64) chunks per sequence, and for most contexts that is not a
-// whole number of workgroups per CU: past 2048 positions at Llama-3-8B,
-// 288-480 workgroups on 256 CUs put a second chunk on some CUs only, and
-// those finish late (10.4-10.8 us at ctx 2304-3584 against 8.1 at 2048).
-// The even split keeps two one-pass workgroups on every CU and the
-// asymmetric merge (9.1-9.9 us).  Shorter chunks than kEvenMinRows were
-// slower than 64-row chunks on fewer CUs (ctx 2048: 8.7 against 8.1 us).
+// chunks of near-equal length (0: use choose_chunk), when each chunk then
+// holds more than kEvenMinRows rows.  Chunks of whole passes leave
+// ceil(T / chunk) chunks per sequence, and for most contexts that is not a
+// whole number of workgroups per CU: at Llama-3-8B, ctx 2304-3584 put a
+// second chunk on some CUs only (10.4-10.8 us against 8.1 at 2048), and ctx
+// 4608-7168 ran 288-448 workgroups of two passes (17.4-19.5 us against
+// 10.3 at 4096).  The even split keeps two workgroups on every CU, with the
+// asymmetric merge while a chunk is one pass (9.0-10.0 us at 2304-3584;
+// 14.3-15.9 us at 4608-7168, where 128 one-pass chunks were slower still).
+// Shorter chunks than kEvenMinRows were slower than 64-row chunks on fewer
+// CUs (ctx 2048: 8.7 against 8.1 us).
 constexpr int kEvenMinRows = 32;
 
 int even_chunks_for(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
@@ -265,8 +267,9 @@ int even_chunks_for(const LaunchShape &s, int n_seq, long long total_rows, int m
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
     const long long per_seq = std::max<long long>(1, (2ll * s.n_cu + n_groups / 2) / n_groups);
     if (per_seq < 2 || per_seq > s.max_chunks) return 0;
-    // exactly one pass per chunk: fixed-size chunks cut the same rows
-    if (max_T <= kEvenMinRows * per_seq || max_T >= pass * per_seq) return 0;
+    if (max_T <= kEvenMinRows * per_seq) return 0;
+    // whole passes per chunk: fixed-size chunks cut the same rows
+    if (max_T % (pass * per_seq) == 0) return 0;
     return (int)per_seq;
 }
 
