@@ -88,8 +88,9 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
                                      # chunks that are not whole 64-row passes (rows past a chunk's
                                      # end masked), with the asymmetric merge at 64 chunks
                                      (3072, 48), (2048, 32), (1000, 40), (130, 8), (4000, 200),
-                                     # automatic: 64 near-equal chunks of 33-64 rows for 8 KV heads
-                                     (2500, 0), (3001, 0)])
+                                     # automatic: 64 near-equal chunks of 33-64 rows for 8 KV heads,
+                                     # then of two passes
+                                     (2500, 0), (3001, 0), (5000, 0)])
 def test_step_shapes_and_splits(nh, nkv, hd, T, split):
     theta = 10000.0 if hd == 64 else 500000.0
     rng = rng_for(nh, nkv, hd, T, split)
@@ -238,6 +239,7 @@ def test_batched_small_ragged_with_tiny_contexts(split):
     (32, 8, 128, [500] * 7 + [5]),       # 64 groups: 8 chunks each, the short sequence 5 chunks of 1 row
     (32, 4, 64, [6000]),                 # 4 groups: 128 near-equal chunks, two-level merge
     (8, 1, 128, [20000]),                # one group: 512 near-equal chunks spread over the XCDs
+    (32, 8, 128, [6000, 5500]),          # 16 groups: 32 near-equal chunks of three passes
 ])
 def test_even_split_chunks(nh, nkv, hd, Ts):
     """Launches that cut each sequence into a fixed number of near-equal
