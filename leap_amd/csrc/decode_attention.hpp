@@ -115,6 +115,15 @@ struct StepArgs {
     float2 *ws_pml;      // [n_groups << spread_log2][G] its (max, sum), log2 units
 };
 
+// Whether a launch runs the PART instance of the decode kernel (the host's
+// choice, restated for the floor kernels, which have no such instance):
+// near-equal chunks, chunks that are not whole passes, or chunks of 2-8
+// passes.
+__host__ __device__ constexpr bool part_launch(int even_chunks, int chunk, int pass)
+{
+    return even_chunks > 0 || chunk % pass != 0 || (chunk >= 2 * pass && chunk <= 8 * pass);
+}
+
 // Chunks of a sequence of T positions, and where chunk c starts: fixed-size
 // chunks of a.chunk rows (the last one shorter), or min(even_chunks, T)
 // chunks of near-equal length, the first T mod n of them one row longer
@@ -311,11 +320,12 @@ struct Shape {
 // MFMAs); false: the same products as per-lane VALU FMAs, leaving the same
 // partial sums in the same lanes (the A/B of the matrix-core choice).
 // PART: chunks that need not be whole passes (near-equal chunks, or forced
-// sizes that are multiples of 8): rows past a chunk's end are masked, and
-// only the chunk holding pos writes the new token.  Launches of whole-pass
-// fixed-size chunks use PART = false, whose prologue is shorter (the two
-// measured 0.07-0.14 us apart per launch at Llama-3-8B ctx 4096 and
-// TinyLlama ctx 256).
+// sizes that are multiples of 8): rows past a chunk's end are masked, only
+// the chunk holding pos writes the new token, and a chunk's passes start at
+// pass chunk_id mod n_sub.  The host also runs it for chunks of 2-8 whole
+// passes, for that rotation.  One-pass and long-run launches use PART =
+// false, whose prologue is shorter (the two measured 0.07-0.14 us apart per
+// launch at Llama-3-8B ctx 4096 and TinyLlama ctx 256).
 template <int HD, int G, int NW, bool MFMA = true, bool PART = false>
 __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
 {
@@ -464,7 +474,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
     const __amdgpu_buffer_rsrc_t vn_rsrc = make_rsrc(v_row_new, new_bytes);
     // (scheduling barriers keep the compiler from reordering the groups)
     float4 tab[NF], knew[NF];
-    load_k(0);
+    // With PART, passes start at pass chunk_id mod n_sub and wrap around.
+    // A launch's chunks start at equal strides, and when the stride is a
+    // power of two the chunks' streams otherwise sit at the same offset of
+    // their rows at once (Llama-3-8B ctx 8192, 128-row chunks: 20.3 -> 17.0
+    // us per launch; 64 q heads: 26.0 -> 18.5 us; ctx 16384: 30.1 -> 26.0).
+    const int sub0 = (PART && n_sub > 1) ? chunk_id % n_sub : 0;
+    load_k(sub0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int f = 0; f < NF; f++) {
@@ -472,7 +488,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
         knew[f] = buf_load4(kn_rsrc, 16u * (uint32_t)(8 * f + ksl));
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_v(0);
+    load_v(sub0);
     const float4 vnew = buf_load4(vn_rsrc, 16u * (uint32_t)vj);
     __builtin_amdgcn_sched_barrier(0);
     rotate_q();
@@ -501,8 +517,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a
 #pragma unroll
         for (int e = 0; e < 4; e++) acc[q][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int sub = 0; sub < n_sub; sub++) {
-        if (sub > 0) {
+    for (int i = 0; i < n_sub; i++) {
+        const int sub = sub0 + i < n_sub ? sub0 + i : sub0 + i - n_sub;
+        if (i > 0) {
             load_k(sub);
             load_v(sub);
         }
@@ -1052,7 +1069,9 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
     const int vg = lane / LPV, vj = lane % LPV;
     const int n_sub = (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS;
     float sum = 0.0f;
-    for (int sub = 0; sub < n_sub; sub++) {
+    const int sub0 = (part_launch(a.even_chunks, a.chunk, S::ROWS) && n_sub > 1) ? chunk_id % n_sub : 0;  // as the step
+    for (int i = 0; i < n_sub; i++) {
+        const int sub = sub0 + i < n_sub ? sub0 + i : sub0 + i - n_sub;
         const int base = chunk_begin + (sub * NW + wave) * R;
         float4 kb[KS][NF], vb[VS];
 #pragma unroll

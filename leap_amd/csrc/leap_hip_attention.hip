@@ -321,7 +321,9 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     const int hd = s.head_dim;
     const int even = even_chunks_for(s, n_seq, total_rows, max_pos + 1);
     const int chunk = even ? (max_pos + even) / even : choose_chunk(s, n_seq, total_rows, max_pos + 1);
-    const bool part = even > 0 || chunk % leap::rows_per_pass(hd, s.group, kWaves) != 0;
+    // The PART instance: chunks that are not whole passes, and chunks of 2-8
+    // passes, whose pass order it rotates.
+    const bool part = leap::part_launch(even, chunk, leap::rows_per_pass(hd, s.group, kWaves));
     KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part);
     if (!fn) return hipErrorInvalidValue;
     const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
