@@ -220,6 +220,34 @@ constexpr int kChunkRows = LEAP_CHUNK_ROWS;  // granularity of the automatic chu
 constexpr int kMinChunk = LEAP_MIN_CHUNK;    // smallest automatic chunk
 constexpr int kSplitRows = 8;                // granularity of any chunk (one MFMA row set)
 
+// A launch of fewer (sequence, KV head) groups than XCDs leaves XCDs idle
+// (a group's chunks share one L2).  When the groups stream at least
+// kSpreadBytes of K/V rows each, each group's chunks are cut into 2, 4 or 8
+// parts, one per XCD, and a second, small launch merges the parts' records
+// across the L2s.  One CU takes in about 30-40 GB/s, so a group's 32 CUs
+// stream 4 MiB in about 3-4 us, and the merge launch costs about 2 us:
+// below that size the launch on fewer XCDs is faster (measured at 1, 2 and
+// 4 KV heads, contexts 512-4096).
+#ifndef LEAP_SPREAD_MIN_BYTES
+#define LEAP_SPREAD_MIN_BYTES (4ll << 20)
+#endif
+constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
+
+// Workgroups per CU in the latency regime: two, except in a launch that
+// spreads its groups over the XCDs, when one per CU gives chunks of two
+// passes or more.  There one per CU measured 3.4-3.8 us faster than
+// one-pass chunks two per CU (one, two and four KV heads at ctx 32768, 16384
+// and 8192) and was no slower at the other sizes measured.
+int latency_per_cu(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
+{
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
+    const long long bytes = total_rows * (long long)s.n_kv_heads * s.head_dim * 8ll;
+    if (!s.ws_parts || n_groups >= leap::kXcds || bytes < n_groups * kSpreadBytes) return 2;
+    const long long per_seq = std::max<long long>(1, (s.n_cu + n_groups / 2) / n_groups);
+    const int pass = leap::rows_per_pass(s.head_dim, s.group, kWaves);
+    return (max_T + per_seq - 1) / per_seq >= 2 * pass ? 1 : 2;
+}
+
 int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
     const int quantum = leap::rows_per_pass(s.head_dim, s.group, kWaves);
@@ -231,7 +259,7 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
     } else {
         const long long bytes = total_rows * kv_dim * 8ll;
         const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
-        const long long per_cu = bytes <= kLatencyBytes ? 2 : ragged ? 12 : 1;
+        const long long per_cu = bytes <= kLatencyBytes ? latency_per_cu(s, n_seq, total_rows, max_T) : ragged ? 12 : 1;
         const long long n_groups = (long long)n_seq * s.n_kv_heads;
         const long long want_wgs = std::max<long long>(1, per_cu * s.n_cu);
         const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
@@ -265,7 +293,8 @@ int even_chunks_for(const LaunchShape &s, int n_seq, long long total_rows, int m
     const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
     if (bytes > kLatencyBytes || ragged) return 0;
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
-    const long long per_seq = std::max<long long>(1, (2ll * s.n_cu + n_groups / 2) / n_groups);
+    const long long per_cu = latency_per_cu(s, n_seq, total_rows, max_T);
+    const long long per_seq = std::max<long long>(1, (per_cu * s.n_cu + n_groups / 2) / n_groups);
     if (per_seq < 2 || per_seq > s.max_chunks) return 0;
     if (max_T <= kEvenMinRows * per_seq) return 0;
     // whole passes per chunk: fixed-size chunks cut the same rows
@@ -299,18 +328,6 @@ MergeFn pick_merge(int hd, int g)
     return nullptr;
 }
 
-// A launch of fewer (sequence, KV head) groups than XCDs leaves XCDs idle
-// (a group's chunks share one L2).  When the groups stream at least
-// kSpreadBytes of K/V rows each, each group's chunks are cut into 2, 4 or 8
-// parts, one per XCD, and a second, small launch merges the parts' records
-// across the L2s.  One CU takes in about 30-40 GB/s, so a group's 32 CUs
-// stream 4 MiB in about 3-4 us, and the merge launch costs about 2 us:
-// below that size the launch on fewer XCDs is faster (measured at 1, 2 and
-// 4 KV heads, contexts 512-4096).
-#ifndef LEAP_SPREAD_MIN_BYTES
-#define LEAP_SPREAD_MIN_BYTES (4ll << 20)
-#endif
-constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
 
 // Enqueue one decode-attention launch.  Returns 0, or a HIP error code
 // (hipErrorInvalidValue for a shape without a kernel or a launch too large).
