@@ -23,7 +23,7 @@ The default run's line also carries, for the same build and box:
     of 64 Llama-3-8B sequences with ragged contexts in [512, 8192], a
     Llama-3-70B pipeline stage (20 layers, batch 16, ctx 8192) and
     Llama-3.1-8B at ctx 131072;
-  - `t_sweep`: microseconds per layer-step over contexts 1 .. 6144 at the
+  - `t_sweep`: microseconds per layer-step over contexts 1 .. 16384 at the
     Llama-3-8B and TinyLlama head shapes, eager and replayed from a HIP graph
     (every decode walks these contexts from position 0);
   - `cpu_baseline`: the reference's own code (oracle/_ref, built from its
@@ -114,7 +114,7 @@ DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
 # the configurations timed beside the headline in the default run
 EXTRA_WORKLOADS = ("tinyllama-ctx256", "llama3-8b-batch64-ragged", "llama3-70b-stage20-batch16",
                    "llama3.1-8b-ctx131072")
-SWEEP_T = (1, 16, 64, 256, 512, 1024, 2048, 2304, 3072, 4096, 6144)
+SWEEP_T = (1, 16, 64, 256, 512, 1024, 2048, 2304, 3072, 4096, 6144, 8192, 16384)
 SWEEP_SHAPES = {"llama3-8b": (32, 32, 8, 128, 500000.0), "tinyllama": (22, 32, 4, 64, 10000.0)}
 
 

@@ -233,6 +233,27 @@ constexpr int kSplitRows = 8;                // granularity of any chunk (one MF
 #endif
 constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
 
+// Whether a decode launch spreads its groups over the XCDs (see
+// launch_attention; it also needs two chunks or more).
+bool spreads(const LaunchShape &s, int n_seq, long long total_rows)
+{
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
+    const long long bytes = total_rows * (long long)s.n_kv_heads * s.head_dim * 8ll;
+    return s.ws_parts && n_groups < leap::kXcds && bytes >= n_groups * kSpreadBytes;
+}
+
+// CUs a launch's workgroups can run on: a (sequence, KV head) group's chunks
+// share one XCD, so a launch of fewer groups than XCDs that does not spread
+// runs on that many XCDs only.  (TinyLlama's four KV heads at ctx 5120-6144
+// were split for all 256 CUs, four workgroups per CU on four XCDs: 17.0-17.2
+// us per layer-step, against 12.0-12.3 us split for their 128 CUs.)
+long long launch_cus(const LaunchShape &s, int n_seq, long long total_rows)
+{
+    const long long n_groups = (long long)n_seq * s.n_kv_heads;
+    if (n_groups >= leap::kXcds || spreads(s, n_seq, total_rows)) return s.n_cu;
+    return std::max<long long>(1, s.n_cu * n_groups / leap::kXcds);
+}
+
 // Workgroups per CU in the latency regime: two, except in a launch that
 // spreads its groups over the XCDs, when one per CU gives chunks of two
 // passes or more.  There one per CU measured 3.4-3.8 us faster than
@@ -241,8 +262,7 @@ constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
 int latency_per_cu(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
-    const long long bytes = total_rows * (long long)s.n_kv_heads * s.head_dim * 8ll;
-    if (!s.ws_parts || n_groups >= leap::kXcds || bytes < n_groups * kSpreadBytes) return 2;
+    if (!spreads(s, n_seq, total_rows)) return 2;
     const long long per_seq = std::max<long long>(1, (s.n_cu + n_groups / 2) / n_groups);
     const int pass = leap::rows_per_pass(s.head_dim, s.group, kWaves);
     return (max_T + per_seq - 1) / per_seq >= 2 * pass ? 1 : 2;
@@ -261,7 +281,7 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
         const long long per_cu = bytes <= kLatencyBytes ? latency_per_cu(s, n_seq, total_rows, max_T) : ragged ? 12 : 1;
         const long long n_groups = (long long)n_seq * s.n_kv_heads;
-        const long long want_wgs = std::max<long long>(1, per_cu * s.n_cu);
+        const long long want_wgs = std::max<long long>(1, per_cu * launch_cus(s, n_seq, total_rows));
         const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
         const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
         c = (int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20);
@@ -294,7 +314,8 @@ int even_chunks_for(const LaunchShape &s, int n_seq, long long total_rows, int m
     if (bytes > kLatencyBytes || ragged) return 0;
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
     const long long per_cu = latency_per_cu(s, n_seq, total_rows, max_T);
-    const long long per_seq = std::max<long long>(1, (per_cu * s.n_cu + n_groups / 2) / n_groups);
+    const long long per_seq =
+        std::max<long long>(1, (per_cu * launch_cus(s, n_seq, total_rows) + n_groups / 2) / n_groups);
     if (per_seq < 2 || per_seq > s.max_chunks) return 0;
     if (max_T <= kEvenMinRows * per_seq) return 0;
     // whole passes per chunk: fixed-size chunks cut the same rows
@@ -347,7 +368,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     if (n_chunk_max > s.max_chunks) return hipErrorInvalidValue;
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
     int spread_log2 = 0;
-    if (kind == kDecode && s.ws_parts && total_rows * s.n_kv_heads * s.head_dim * 8ll >= n_groups * kSpreadBytes)
+    if (kind == kDecode && spreads(s, n_seq, total_rows))
         while (n_groups << (spread_log2 + 1) <= leap::kXcds && n_chunk_max >= (2 << spread_log2)) spread_log2++;
     const int grid_x = (n_chunk_max + (1 << spread_log2) - 1) >> spread_log2;  // chunks per part
 
