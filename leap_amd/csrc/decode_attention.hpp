@@ -327,7 +327,7 @@ struct Shape {
 // false, whose prologue is shorter (the two measured 0.07-0.14 us apart per
 // launch at Llama-3-8B ctx 4096 and TinyLlama ctx 256).
 template <int HD, int G, int NW, bool MFMA = true, bool PART = false>
-__global__ __launch_bounds__(NW * kWave) void decode_attention_kernel(StepArgs a)
+__global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
