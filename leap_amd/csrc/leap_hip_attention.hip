@@ -209,16 +209,10 @@ LaunchShape shape_of(const leap_hip_attention *h)
 //     start are short.
 // The sequence length (the mean one when ragged) is cut into equal chunks,
 // rounded up to whole passes; at most s.max_chunks chunks per sequence.
+// Equal-length sequences in the latency regime are cut into near-equal
+// chunks instead when that keeps every CU busy (even_chunks_for).
 constexpr long long kLatencyBytes = 128ll << 20;
-#ifndef LEAP_CHUNK_ROWS
-#define LEAP_CHUNK_ROWS 64
-#endif
-#ifndef LEAP_MIN_CHUNK
-#define LEAP_MIN_CHUNK 64
-#endif
-constexpr int kChunkRows = LEAP_CHUNK_ROWS;  // granularity of the automatic chunk sizes
-constexpr int kMinChunk = LEAP_MIN_CHUNK;    // smallest automatic chunk
-constexpr int kSplitRows = 8;                // granularity of any chunk (one MFMA row set)
+constexpr int kSplitRows = 8;  // granularity of any chunk (one MFMA row set)
 
 // A launch of fewer (sequence, KV head) groups than XCDs leaves XCDs idle
 // (a group's chunks share one L2).  When the groups stream at least
@@ -228,10 +222,7 @@ constexpr int kSplitRows = 8;                // granularity of any chunk (one MF
 // stream 4 MiB in about 3-4 us, and the merge launch costs about 2 us:
 // below that size the launch on fewer XCDs is faster (measured at 1, 2 and
 // 4 KV heads, contexts 512-4096).
-#ifndef LEAP_SPREAD_MIN_BYTES
-#define LEAP_SPREAD_MIN_BYTES (4ll << 20)
-#endif
-constexpr long long kSpreadBytes = LEAP_SPREAD_MIN_BYTES;  // per group
+constexpr long long kSpreadBytes = 4ll << 20;  // per group
 
 // Whether a decode launch spreads its groups over the XCDs (see
 // launch_attention; it also needs two chunks or more).
@@ -284,8 +275,7 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         const long long want_wgs = std::max<long long>(1, per_cu * launch_cus(s, n_seq, total_rows));
         const long long per_seq = std::max<long long>(1, (want_wgs + n_groups / 2) / n_groups);
         const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
-        c = (int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20);
-        c = c > quantum ? round_up(c, quantum) : std::max(kMinChunk, round_up(c, kChunkRows));
+        c = round_up((int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20), quantum);
         c = std::min(c, round_up(max_T, quantum));
     }
     return std::max(c, std::max(floor_chunk, kSplitRows));
