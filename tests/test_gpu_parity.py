@@ -382,6 +382,44 @@ def test_random_shapes_positions_and_batches(nh, nkv, hd, T, split, batch):
             _step_and_check(att, 0, int(pos[i]), q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
 
 
+def _random_cases_long(n, seed):
+    """Seeded draws reaching the launch shapes of longer contexts: near-equal
+    chunks of one to several passes (their pass order rotated), spread
+    launches of few KV heads, forced chunk sizes that are not whole passes,
+    and batches of near-equal lengths (cut into near-equal chunks too)."""
+    shapes = [(32, 8, 128), (24, 8, 128), (16, 16, 64), (32, 4, 64), (64, 8, 128), (8, 8, 128),
+              (16, 2, 128), (12, 4, 64), (8, 1, 64), (8, 1, 128), (32, 4, 128)]
+    rng = np.random.default_rng(seed)
+    for i in range(n):
+        nh, nkv, hd = shapes[rng.integers(len(shapes))]
+        T = int(rng.choice([rng.integers(2000, 20000), rng.integers(1, 3000)]))
+        split = int(rng.choice([0, 0, 0, 8, 24, 40, 72, 136, 200]))
+        batch = int(rng.choice([1, 1, 2, 4]))
+        even = bool(rng.integers(2))
+        yield pytest.param(nh, nkv, hd, T, split, batch, even,
+                           id=f"{i}-{nh}x{nkv}x{hd}-T{T}-s{split}-b{batch}-{'even' if even else 'ragged'}")
+
+
+@pytest.mark.parametrize("nh,nkv,hd,T,split,batch,even", list(_random_cases_long(40, 0x10A6)))
+def test_random_long_contexts_and_chunkings(nh, nkv, hd, T, split, batch, even):
+    """As test_random_shapes_positions_and_batches over longer contexts and
+    finer forced chunk sizes; a batch's other sequences sit within 1/8 of
+    the longest (even) or anywhere below it."""
+    rng = rng_for(nh, nkv, hd, T, split, batch, int(even), 78)
+    with HipAttention(nh, nkv, hd, T, max_batch=batch) as att:
+        att.kv_fill_normal(int(rng.integers(1 << 30)), 1.0 / np.sqrt(hd))
+        if split:
+            att.set_split(split)
+        lo = T - 1 - T // 8 if even else 0
+        pos = np.concatenate([[T - 1], rng.integers(lo, T, size=batch - 1)]).astype(np.int32)
+        q = normal(rng, (batch, nh * hd), hd)
+        k = normal(rng, (batch, nkv * hd), hd)
+        v = normal(rng, (batch, nkv * hd), hd)
+        out = att.step(0, int(pos[0]), q[0], k[0], v[0])[None] if batch == 1 else att.step_batched(0, pos, q, k, v)
+        for i in range(batch):
+            _step_and_check(att, 0, int(pos[i]), q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
 # ---- few KV heads: a group's chunks spread over several XCDs ------------------------
 
 @pytest.mark.parametrize("nh,nkv,hd,T,split", [
