@@ -138,8 +138,8 @@ constexpr int kThreads = kWaves * leap::kWave;
 // grid (measurement only).
 enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
 
-// part: chunks that are not all whole passes (near-equal chunks, or a forced
-// size that is not a multiple of a pass).
+// part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
+// long (leap::part_launch).
 KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false, bool part = false)
 {
 #define LEAP_CASE(HD, G)                                                                                   \
@@ -396,10 +396,12 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     const long long n_pgroups = n_groups << spread_log2;
     const long long n_wg = (n_pgroups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
     if (n_wg > 0x7fffffffLL) return hipErrorInvalidValue;
-    // One pass per workgroup and at least two workgroups per CU: a CU's
-    // second workgroup receives its rows after its first, so each group's
-    // first-dispatched half of chunks can fold while the rest streams.
-    a.merge_asym = (chunk <= leap::rows_per_pass(hd, s.group, kWaves) && n_pgroups * grid_x >= 2LL * s.n_cu) ? 1 : 0;
+    // One pass per workgroup and at least two workgroups per CU of the XCDs
+    // the launch runs on: a CU's second workgroup receives its rows after
+    // its first, so each group's first-dispatched half of chunks can fold
+    // while the rest streams.
+    a.merge_asym = (chunk <= leap::rows_per_pass(hd, s.group, kWaves) &&
+                    n_pgroups * grid_x >= 2LL * launch_cus(s, n_seq, total_rows)) ? 1 : 0;
     hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
     MergeFn mf = pick_merge(hd, s.group);
