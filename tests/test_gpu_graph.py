@@ -30,13 +30,17 @@ def _capture(fn, stream):
     return graph
 
 
-def test_step_loop_replays_match_eager(hip_device):
+@pytest.mark.parametrize("nh,nkv,hd,sl,pos,poss", [
+    (32, 8, 128, 3100, 2999, (2999, 17, 1200)),    # near-equal chunks of one pass, asymmetric merge
+    (32, 8, 128, 8200, 8191, (8191, 8000, 300)),   # 128-row chunks of two passes, rotated
+    (8, 1, 128, 20000, 19999, (19999, 5000, 40)),  # one KV head spread over the XCDs: two launches per step
+])
+def test_step_loop_replays_match_eager(hip_device, nh, nkv, hd, sl, pos, poss):
     """Four layers of single-sequence steps (split-K merge over several
     chunks) and four of a ragged batch, captured once and replayed."""
     import torch
-    nh, nkv, hd, L, sl, batch = 32, 8, 128, 4, 3100, 3
-    pos = 2999
-    poss = np.array([2999, 17, 1200], np.int32)
+    L, batch = 4, 3
+    poss = np.array(poss, np.int32)
     with HipAttention(nh, nkv, hd, sl, n_layers=L, max_batch=batch) as att:
         att.kv_fill_normal(21, 1.0 / np.sqrt(hd))
         g = torch.Generator(device="cuda:0")
