@@ -273,6 +273,16 @@ __device__ __forceinline__ void scale4(float4 &acc, float s)
     acc.w *= s;
 }
 
+// Lane src's float4 (every lane of the wave active).
+__device__ __forceinline__ float4 lane_float4(float4 v, int src)
+{
+    const int b = src * 4;
+    return make_float4(__int_as_float(__builtin_amdgcn_ds_bpermute(b, __float_as_int(v.x))),
+                       __int_as_float(__builtin_amdgcn_ds_bpermute(b, __float_as_int(v.y))),
+                       __int_as_float(__builtin_amdgcn_ds_bpermute(b, __float_as_int(v.z))),
+                       __int_as_float(__builtin_amdgcn_ds_bpermute(b, __float_as_int(v.w))));
+}
+
 // Interleaved-pair rotation of one float4 (two pairs) with table entry
 // t = (cos_a, sin_a, cos_b, sin_b), products rounded separately as the
 // reference's mul/mul/addsub body does (FloatTransformer.cpp:461-464).
@@ -423,10 +433,10 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 #pragma unroll
     for (int i = 0; i < QP; i++) {
         const int pair = tid + i * S::THREADS;
-        if (pair < PAIRS) {
-            qp[i] = reinterpret_cast<const float2 *>(qg)[pair];
-            qt[i] = rope2[pair % (HD / 2)];
-        }
+        if (pair < PAIRS) qp[i] = reinterpret_cast<const float2 *>(qg)[pair];
+        // every thread: lane L holds table pair L mod HD/2 (THREADS is a
+        // multiple of HD/2), which the new token's k rotation reads too
+        qt[i] = rope2[pair % (HD / 2)];
     }
     float4 kb[KS][NF], vb[VS];
     auto load_k = [&](int sub) {
@@ -462,36 +472,42 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         }
     };
 
-    // First tile, in the order q (above), K rows, the new token's k and its
-    // table entries, V rows, the new token's v.  Every workgroup issues the
-    // new token's loads, through descriptors that are empty outside the
-    // workgroup holding pos (those loads return 0 without touching memory):
-    // without a branch, the waits (which count outstanding loads in issue
-    // order) stay exact, and the prologue barrier waits for q alone.
+    // First tile, in the order q and its table pairs (above), the new
+    // token's k, K rows, V rows, the new token's v.  Every workgroup issues
+    // the new token's loads, one per wave each, through descriptors that are
+    // empty outside the workgroup holding pos (those loads return 0 without
+    // touching memory): without a branch, the waits (which count outstanding
+    // loads in issue order) stay exact, and the prologue barrier waits for q
+    // alone.  The wave holding pos takes its lanes' parts of the k row
+    // through LDS, next to the table row (the q pairs' table entries), and
+    // of the v row across lanes.
     const uint32_t new_bytes = has_pos ? (uint32_t)HD * 4u : 0u;
-    const __amdgpu_buffer_rsrc_t tab_rsrc = make_rsrc(rope_row, new_bytes);
     const __amdgpu_buffer_rsrc_t kn_rsrc = make_rsrc(k_row_new, new_bytes);
     const __amdgpu_buffer_rsrc_t vn_rsrc = make_rsrc(v_row_new, new_bytes);
     // (scheduling barriers keep the compiler from reordering the groups)
-    float4 tab[NF], knew[NF];
     // With PART, passes start at pass chunk_id mod n_sub and wrap around.
     // A launch's chunks start at equal strides, and when the stride is a
     // power of two the chunks' streams otherwise sit at the same offset of
     // their rows at once (Llama-3-8B ctx 8192, 128-row chunks: 20.3 -> 17.0
     // us per launch; 64 q heads: 26.0 -> 18.5 us; ctx 16384: 30.1 -> 26.0).
     const int sub0 = (PART && n_sub > 1) ? chunk_id % n_sub : 0;
+    // lane L < HD/4 holds float4 L of k_new (of v_new below), the other
+    // lanes read past the range, 0; k_new goes ahead of the K rows, so that
+    // the wave holding pos has it staged before its rows arrive
+    const float4 knew_l = buf_load4(kn_rsrc, 16u * (uint32_t)lane);
+    __builtin_amdgcn_sched_barrier(0);
     load_k(sub0);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int f = 0; f < NF; f++) {
-        tab[f] = buf_load4(tab_rsrc, 16u * (uint32_t)(8 * f + ksl));
-        knew[f] = buf_load4(kn_rsrc, 16u * (uint32_t)(8 * f + ksl));
-    }
-    __builtin_amdgcn_sched_barrier(0);
     load_v(sub0);
-    const float4 vnew = buf_load4(vn_rsrc, 16u * (uint32_t)vj);
+    const float4 vnew_l = buf_load4(vn_rsrc, 16u * (uint32_t)lane);
     __builtin_amdgcn_sched_barrier(0);
     rotate_q();
+    // The table row, for the new token's k, in this wave's combine buffer
+    // (unused until the waves combine): float4 [D4, 2*D4); the k_new row
+    // goes to [0, D4) when it is needed.
+    float4 *nt_lds = &comb_o[wave][0][0][0];
+    static_assert(RPV * G >= 2, "new-token staging");
+    if (lane < HD / 2) reinterpret_cast<float2 *>(nt_lds + D4)[lane] = qt[0];
     __syncthreads();
     // Score MFMA A operand: head 4*quad + kj at this lane's dims (zero for
     // the unused heads of a partial quad).
@@ -532,14 +548,27 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         // weighted V (it is loaded last): overwriting a register whose load
         // is still in flight, or storing a loaded value, first waits for
         // that load.
+        const bool pos_here = (!PART || has_pos) && pos >= base && pos < base + R;  // wave-uniform
+        if (pos_here) {
+            // k_new through the wave's staging: each lane reads its dims
+            // 32*f + 4*ksl .. +3 of k_new and of the table row
+            if (lane < D4) nt_lds[lane] = knew_l;
+            __builtin_amdgcn_wave_barrier();
+            float4 knew[NF], tab[NF];
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            const int t = base + ks * 8 + krow;
-            if ((!PART || has_pos) && t == pos) {
+            for (int f = 0; f < NF; f++) {
+                knew[f] = nt_lds[8 * f + ksl];
+                tab[f] = nt_lds[D4 + 8 * f + ksl];
+            }
 #pragma unroll
-                for (int f = 0; f < NF; f++) {
-                    kb[ks][f] = rope4(knew[f], tab[f]);
-                    *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = kb[ks][f];
+            for (int ks = 0; ks < KS; ks++) {
+                const int t = base + ks * 8 + krow;
+                if (t == pos) {
+#pragma unroll
+                    for (int f = 0; f < NF; f++) {
+                        kb[ks][f] = rope4(knew[f], tab[f]);
+                        *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = kb[ks][f];
+                    }
                 }
             }
         }
@@ -638,9 +667,15 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 #pragma unroll
         for (int vs = 0; vs < VS; vs++) {
             const int r = vs * RPV + vg;
-            if ((!PART || has_pos) && base + r == pos) {
-                vb[vs] = vnew;
-                *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
+            // the load set holding pos (wave-uniform) reads v_new's float4
+            // vj across the wave, at this set: its wait for the v_new load,
+            // issued last, then holds up only this set's products
+            if (pos_here && pos - base >= vs * RPV && pos - base < (vs + 1) * RPV) {
+                const float4 vnew = lane_float4(vnew_l, vj);
+                if (base + r == pos) {
+                    vb[vs] = vnew;
+                    *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
+                }
             }
 #pragma unroll
             for (int q = 0; q < GQ; q++) {
