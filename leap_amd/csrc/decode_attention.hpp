@@ -49,7 +49,7 @@ constexpr int kWave = 64;
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
 constexpr int kSubGroup = 8;              // chunks per first-level merge
 constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
-constexpr int kFinalMax = 32 + 32 / kSubGroup;  // records of the asymmetric merge's final fold (64 chunks)
+constexpr int kFinalMax = 40;  // records of a one-level fold: the asymmetric merge's 36 at 64 chunks, or up to 40 chunks
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
@@ -813,16 +813,17 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
             mm = m_new;
         }
     };
-    // Fold records [first, first + n), n <= MG * BW a compile-time count
-    // (std::integral_constant), as one batch of loads: record lane mg takes
-    // records mg, mg + MG, ..., and the lanes meet in LDS.  Leaves (ox, Mx,
-    // Lx) in the threads with mg == 0.  With n known, every load a lane
-    // issues is unconditional and exactly the records it needs.  The (max,
-    // sum) pairs, which the D4 lanes of a record lane all need, are loaded
-    // once per (head, record) across the workgroup, ahead of the partial
-    // outputs, and shared through LDS: a load of each pair in every lane
-    // that needs it cost about 0.5 us at Llama-3-8B ctx 4096.
-    auto fold_wide = [&](int first, auto n_c, float4 &ox, float &Mx, float &Lx) {
+    // Fold records [first, first + n_rt), n_rt <= n, n <= MG * BW a
+    // compile-time count (std::integral_constant), as one batch of loads:
+    // record lane mg takes records mg, mg + MG, ..., and the lanes meet in
+    // LDS.  Leaves (ox, Mx, Lx) in the threads with mg == 0.  With n known,
+    // every load a lane issues is unconditional; records [n_rt, n) read past
+    // the range (0) and count as empty.  The (max, sum) pairs, which the D4
+    // lanes of a record lane all need, are loaded once per (head, record)
+    // across the workgroup, ahead of the partial outputs, and shared through
+    // LDS: a load of each pair in every lane that needs it cost about 0.5 us
+    // at Llama-3-8B ctx 4096.
+    auto fold_wide = [&](int first, auto n_c, int n_rt, float4 &ox, float &Mx, float &Lx) {
         constexpr int n = decltype(n_c)::value;
         static_assert(n <= MG * BW && n <= kFinalMax, "records per lane");
         constexpr int BL = (n + MG - 1) / MG;  // records per lane
@@ -832,7 +833,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 #pragma unroll
         for (int i = 0; i < MLT; i++) {
             const int t = tid + i * S::THREADS, h = t / n, c = t % n;
-            const bool in = t < NML && h < G;
+            const bool in = t < NML && h < G && c < n_rt;
             mlv[i] = buf_load2<kSc1>(wm_rsrc, in ? (uint32_t)(h * n_rec + first + c) * 8u : ws_ml_bytes);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -841,28 +842,33 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         for (int j = 0; j < BL; j++) {
             const int c = mg + j * MG;
             const uint32_t row = (uint32_t)(mh * n_rec + first + c);
-            const bool in = live && c < n;
+            const bool in = live && c < n_rt;
             ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < MLT; i++)
-            if (tid + i * S::THREADS < NML) ml_lds[tid + i * S::THREADS] = mlv[i];
+        for (int i = 0; i < MLT; i++) {
+            const int t = tid + i * S::THREADS;
+            if (t < NML) ml_lds[t] = (t % n < n_rt) ? mlv[i] : make_float2(-INFINITY, 0.f);
+        }
         __syncthreads();
         float2 mlb[BL];
 #pragma unroll
         for (int j = 0; j < BL; j++) {
             const int c = mg + j * MG;
-            mlb[j] = c < n ? ml_lds[mh * n + c] : make_float2(0.f, 0.f);
+            mlb[j] = c < n ? ml_lds[mh * n + c] : make_float2(-INFINITY, 0.f);
         }
         float mm = -INFINITY, ll = 0.f;
         float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int j = 0; j < BL; j++)
             if (mg + j * MG < n) mm = fmaxf(mm, mlb[j].x);
+        // a lane whose records are all empty keeps mm = -inf; its weights
+        // exp2(-inf - 0) are 0
+        const float mref = (mm == -INFINITY) ? 0.f : mm;
 #pragma unroll
         for (int j = 0; j < BL; j++) {
-            const float w = (mg + j * MG < n) ? fast_exp2(mlb[j].x - mm) : 0.f;
+            const float w = (mg + j * MG < n) ? fast_exp2(mlb[j].x - mref) : 0.f;
             fma4(oo, w, ob[j]);
             ll += w * mlb[j].y;
         }
@@ -968,9 +974,46 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         if (tid == 0) ctr[0] = 0;
         float4 of;
         float Mf, Lf;
-        fold_wide(half, std::integral_constant<int, n_final>{}, of, Mf, Lf);
+        fold_wide(half, std::integral_constant<int, n_final>{}, n_final, of, Mf, Lf);
         if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
     };
+    // One level for launches without the asymmetric shape and 9-40 chunks:
+    // every chunk counts into the final counter and the last folds all
+    // records as one batch of loads, compiled for NC = n_local rounded up to
+    // a multiple of 8 (the records past n_local are empty).  Against the
+    // two-level tree (sub-groups of 8, then their records) this leaves out a
+    // store, drain and atomic round trip for 8-40 KiB more loads into the
+    // last CU: Llama-3-8B ctx 1024 8.03 -> 6.77 us, ctx 2048 8.33 -> 7.58 us.
+    auto merge_flat = [&](auto nc_c) {
+        constexpr int NC = decltype(nc_c)::value;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            s_last = (prev == n_local - 1);
+        }
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) ctr[0] = 0;
+        float4 of;
+        float Mf, Lf;
+        fold_wide(0, std::integral_constant<int, NC>{}, n_local, of, Mf, Lf);
+        if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
+    };
+    if (!a.merge_asym && n_local > B) {
+        if constexpr (16 <= MG * BW) {
+            if (n_local <= 16) return merge_flat(std::integral_constant<int, 16>{});
+        }
+        if constexpr (24 <= MG * BW) {
+            if (n_local <= 24) return merge_flat(std::integral_constant<int, 24>{});
+        }
+        if constexpr (32 <= MG * BW) {
+            if (n_local <= 32) return merge_flat(std::integral_constant<int, 32>{});
+        }
+        if constexpr (40 <= MG * BW) {
+            if (n_local <= 40) return merge_flat(std::integral_constant<int, 40>{});
+        }
+    }
     if (a.merge_asym) {
         if constexpr (32 + 4 <= MG * BW) {
             if (n_local == 64) return merge_asym(std::integral_constant<int, 64>{});

@@ -88,6 +88,9 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
                                      # chunks that are not whole 64-row passes (rows past a chunk's
                                      # end masked), with the asymmetric merge at 64 chunks
                                      (3072, 48), (2048, 32), (1000, 40), (130, 8), (4000, 200),
+                                     # 10 and 38 chunks without the asymmetric shape: one-level
+                                     # folds compiled for 16 and 40 records, the rest empty
+                                     (600, 64), (2400, 64),
                                      # automatic: 64 near-equal chunks of 33-64 rows for 8 KV heads,
                                      # then of two passes
                                      (2500, 0), (3001, 0), (5000, 0)])
