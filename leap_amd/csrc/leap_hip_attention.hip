@@ -396,11 +396,14 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     const long long n_pgroups = n_groups << spread_log2;
     const long long n_wg = (n_pgroups + leap::kXcds - 1) / leap::kXcds * leap::kXcds * grid_x;
     if (n_wg > 0x7fffffffLL) return hipErrorInvalidValue;
-    // One pass per workgroup and at least two workgroups per CU of the XCDs
-    // the launch runs on: a CU's second workgroup receives its rows after
-    // its first, so each group's first-dispatched half of chunks can fold
-    // while the rest streams.
-    a.merge_asym = (chunk <= leap::rows_per_pass(hd, s.group, kWaves) &&
+    // At least two workgroups per CU of the XCDs the launch runs on, each of
+    // at most 8 passes: a CU's second workgroup receives its rows after its
+    // first (with several passes, each of its passes after the first's), so
+    // each group's first-dispatched half of chunks can fold while the rest
+    // streams.  Chunks of 2-8 passes at Llama-3-8B, against the two-level
+    // tree: ctx 4608 13.48 -> 12.78 us, 8192 16.41 -> 15.86, 16384 25.57 ->
+    // 25.04 us.
+    a.merge_asym = (chunk <= 8 * leap::rows_per_pass(hd, s.group, kWaves) &&
                     n_pgroups * grid_x >= 2LL * launch_cus(s, n_seq, total_rows)) ? 1 : 0;
     hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
