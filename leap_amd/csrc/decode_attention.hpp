@@ -141,6 +141,7 @@ __device__ __forceinline__ int chunk_start(const StepArgs &a, int T, int n_chunk
     return min(c * a.chunk, T);
 }
 
+
 // ---- buffer access ------------------------------------------------------------
 //
 // Raw buffer loads take 32-bit byte offsets from a base and return zero past
@@ -490,6 +491,9 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     // power of two the chunks' streams otherwise sit at the same offset of
     // their rows at once (Llama-3-8B ctx 8192, 128-row chunks: 20.3 -> 17.0
     // us per launch; 64 q heads: 26.0 -> 18.5 us; ctx 16384: 30.1 -> 26.0).
+    // Rotating among the full passes only, so that a partial last pass is
+    // never the first (whose loads cannot be skipped), measured slower at
+    // ctx 8200 and 12000 (+0.2 and +0.5 us): fewer phases among the chunks.
     const int sub0 = (PART && n_sub > 1) ? chunk_id % n_sub : 0;
     // lane L < HD/4 holds float4 L of k_new (of v_new below), the other
     // lanes read past the range, 0; k_new goes ahead of the K rows, so that
@@ -535,11 +539,16 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 
     for (int i = 0; i < n_sub; i++) {
         const int sub = sub0 + i < n_sub ? sub0 + i : sub0 + i - n_sub;
+        const int base = chunk_begin + (sub * NW + wave) * R;
+        // A later pass whose rows for this wave all lie past the chunk's end
+        // (the partial last pass) is skipped by the wave: no loads, nothing
+        // to add.  Every load of the earlier passes has been waited for, so
+        // both ways leave the same loads outstanding.
+        if (PART && i > 0 && base >= chunk_end) continue;
         if (i > 0) {
             load_k(sub);
             load_v(sub);
         }
-        const int base = chunk_begin + (sub * NW + wave) * R;
 
         // The new token's row: k_new, rotated exactly as the reference
         // rotates it (it is stored), and v_new are appended to
@@ -1147,10 +1156,13 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
     const int vg = lane / LPV, vj = lane % LPV;
     const int n_sub = (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS;
     float sum = 0.0f;
-    const int sub0 = (part_launch(a.even_chunks, a.chunk, S::ROWS) && n_sub > 1) ? chunk_id % n_sub : 0;  // as the step
+    // passes and skips as the step
+    const bool part = part_launch(a.even_chunks, a.chunk, S::ROWS);
+    const int sub0 = (part && n_sub > 1) ? chunk_id % n_sub : 0;
     for (int i = 0; i < n_sub; i++) {
         const int sub = sub0 + i < n_sub ? sub0 + i : sub0 + i - n_sub;
         const int base = chunk_begin + (sub * NW + wave) * R;
+        if (part && i > 0 && base >= chunk_end) continue;
         float4 kb[KS][NF], vb[VS];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++)
