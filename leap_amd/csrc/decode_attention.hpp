@@ -344,6 +344,14 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
     constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, GM = S::GM, MG = S::MG;
 
+    // The argument block's fields that the prologue reads, loaded as one
+    // batch before the first branch (an empty asm that takes them as
+    // inputs): left to the compiler, each load follows the branch that first
+    // needs it, one dependent round trip after another.
+    asm volatile("" ::"s"(a.q), "s"(a.k_new), "s"(a.v_new), "s"(a.k_cache), "s"(a.v_cache), "s"(a.rope),
+                 "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar), "s"(a.max_pos), "s"(a.seq_len),
+                 "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks), "s"(a.n_groups),
+                 "s"(a.spread_log2), "s"(a.even_chunks));
     // id = ((pg / 8) * grid_chunks + lc) * 8 + pg % 8, where the part-group
     // pg = group * 2^spread_log2 + part covers the group's chunks
     // [part * grid_chunks, (part + 1) * grid_chunks) and lc is the chunk
