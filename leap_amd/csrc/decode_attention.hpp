@@ -1093,6 +1093,10 @@ template <int HD, int G>
 __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
 {
     constexpr int D4 = HD / 4;
+    // the argument block as one batch of loads, as in the decode kernel
+    asm volatile("" ::"s"(a.pos_dev), "s"(a.ws_po), "s"(a.ws_pml), "s"(a.out), "s"(a.pos_scalar), "s"(a.max_pos),
+                 "s"(a.seq_len), "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
+                 "s"(a.n_groups), "s"(a.spread_log2), "s"(a.even_chunks));
     const int group = blockIdx.x;
     if (group >= a.n_groups) return;
     const int seq = group / a.n_kv_heads, kvh = group % a.n_kv_heads;
@@ -1140,6 +1144,10 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
     constexpr int NF = S::NF, R = S::R, KS = S::KS, LPV = S::LPV, RPV = S::RPV, VS = S::VS;
+    // the argument block as one batch of loads, as in the decode kernel
+    asm volatile("" ::"s"(a.k_cache), "s"(a.v_cache), "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar),
+                 "s"(a.max_pos), "s"(a.seq_len), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
+                 "s"(a.n_groups), "s"(a.even_chunks));
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
     const int chunk_id = local % a.grid_chunks;
