@@ -994,13 +994,15 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         fold_wide(half, std::integral_constant<int, n_final>{}, n_final, of, Mf, Lf);
         if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
     };
-    // One level for launches without the asymmetric shape and 9-40 chunks:
+    // One level for launches without the asymmetric shape and 2-40 chunks:
     // every chunk counts into the final counter and the last folds all
     // records as one batch of loads, compiled for NC = n_local rounded up to
     // a multiple of 8 (the records past n_local are empty).  Against the
     // two-level tree (sub-groups of 8, then their records) this leaves out a
     // store, drain and atomic round trip for 8-40 KiB more loads into the
     // last CU: Llama-3-8B ctx 1024 8.03 -> 6.77 us, ctx 2048 8.33 -> 7.58 us.
+    // Up to 8 chunks it replaces a fold in the threads of one record lane,
+    // which loaded each (max, sum) pair in every lane: ctx 256 6.60 -> 6.52.
     auto merge_flat = [&](auto nc_c) {
         constexpr int NC = decltype(nc_c)::value;
         __builtin_amdgcn_s_waitcnt(0);
@@ -1017,7 +1019,8 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         fold_wide(0, std::integral_constant<int, NC>{}, n_local, of, Mf, Lf);
         if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
     };
-    if (!a.merge_asym && n_local > B) {
+    if (!a.merge_asym && n_local > 1) {
+        if (n_local <= 8) return merge_flat(std::integral_constant<int, 8>{});
         if constexpr (16 <= MG * BW) {
             if (n_local <= 16) return merge_flat(std::integral_constant<int, 16>{});
         }
