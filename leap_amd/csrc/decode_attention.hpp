@@ -12,20 +12,20 @@
 //     128-bit buffer loads, and every wave serves all q heads of the KV group
 //     from those registers: GQA score (:496-630), online softmax (running
 //     max / sum, :216-238) and the weighted-V accumulation (:634-661);
-//   - the merge of the chunk partials, as a two-level arrival tree: each chunk
-//     writes an unnormalised partial (o, max, sum) and counts itself in on its
-//     sub-group's counter (kSubGroup consecutive chunks); the last arrival of a
-//     sub-group folds that sub-group's partials into one record and counts in
-//     on the final counter, whose last arrival folds the sub-group records
-//     into the output.  Each counter sees at most kSubGroup (or
-//     kMaxChunks / kSubGroup) arrivals and each fold reads a few KB, instead of one workgroup pulling
-//     every partial through a single CU.
-//   - when every CU runs two one-pass workgroups of the launch, a CU receives
-//     its data in issue order, so the first-dispatched half of a group's chunks
-//     finishes about half a stream earlier than the rest.  That half folds in
-//     sub-groups while the stream runs; the second half counts straight into
-//     the final counter, whose last arrival folds the second half's chunk
-//     records and the first half's sub-group records in one level.
+//   - the merge of the chunk partials by arrival counters in L2: each chunk
+//     writes an unnormalised partial (o, max, sum) and counts itself in; the
+//     last arrival folds.  Up to 40 chunks, every chunk counts into the final
+//     counter and its last arrival folds all records as one batch of loads.
+//     When every CU runs two workgroups of the launch, a CU receives its data
+//     in issue order, so the first-dispatched half of a group's chunks
+//     finishes earlier than the rest: that half folds in sub-groups of
+//     kSubGroup while the stream runs, and the second half counts straight
+//     into the final counter, whose last arrival folds the second half's
+//     chunk records and the first half's sub-group records in one level.
+//     Otherwise (more chunks, or 4 KiB records) a two-level tree: sub-groups
+//     of kSubGroup consecutive chunks fold into one record each, and the last
+//     sub-group to finish folds those.  No fold pulls more than about 80 KiB
+//     through one CU.
 //
 // XCD placement.  Workgroups are dealt to the XCDs round-robin by workgroup
 // id, so id % 8 names the XCD (the same holds within a 1-, 2- or 4-XCD
@@ -49,7 +49,7 @@ constexpr int kWave = 64;
 constexpr int kMaxChunks = 512;           // split-K chunks per (sequence, KV head)
 constexpr int kSubGroup = 8;              // chunks per first-level merge
 constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
-constexpr int kFinalMax = 40;  // records of a one-level fold: the asymmetric merge's 36 at 64 chunks, or up to 40 chunks
+constexpr int kFinalMax = 40;            // records of a one-level fold (the asymmetric merge's 36 at 64 chunks)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
