@@ -277,6 +277,19 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         const long long len = ragged ? (total_rows + n_seq - 1) / n_seq : max_T;
         c = round_up((int)std::min<long long>((len + per_seq - 1) / per_seq, 1 << 20), quantum);
         c = std::min(c, round_up(max_T, quantum));
+        // Short contexts: 2-4 one-pass chunks per group (2-8 with at most 4 q
+        // heads per KV head at head_dim 128) leave most CUs idle, and each CU
+        // takes in its chunk at the rate one CU reads.  Half-pass chunks put
+        // twice the CUs on the stream for twice the records in the one-level
+        // merge (Llama-3-8B ctx 128 6.48 -> 6.11, 256 6.49 -> 6.16, 512 6.54
+        // -> 6.27 us; 64 q heads at ctx 256 7.60 -> 7.21 us).  At 12 or more
+        // chunks, or once the halved launch would fill more than half the
+        // CUs, they measured slower.
+        const long long n_chunks = (max_T + quantum - 1) / quantum;
+        const bool few = n_chunks <= 4 || (n_chunks <= 8 && s.group <= 4 && s.head_dim == 128);
+        if (bytes <= kLatencyBytes && !ragged && c == quantum && n_chunks >= 2 && few &&
+            4 * n_chunks * n_groups <= launch_cus(s, n_seq, total_rows))
+            c = quantum / 2;
     }
     return std::max(c, std::max(floor_chunk, kSplitRows));
 }
