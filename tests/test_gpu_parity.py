@@ -93,7 +93,10 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
                                      (600, 64), (2400, 64),
                                      # automatic: 64 near-equal chunks of 33-64 rows for 8 KV heads,
                                      # then of two passes
-                                     (2500, 0), (3001, 0), (5000, 0)])
+                                     (2500, 0), (3001, 0), (5000, 0),
+                                     # automatic short contexts: half-pass chunks where a group has
+                                     # 2-8 one-pass chunks and the launch leaves CUs idle
+                                     (100, 0), (256, 0), (500, 0)])
 def test_step_shapes_and_splits(nh, nkv, hd, T, split):
     theta = 10000.0 if hd == 64 else 500000.0
     rng = rng_for(nh, nkv, hd, T, split)
