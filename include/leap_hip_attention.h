@@ -311,6 +311,16 @@ int leap_hip_attention_set_split(leap_hip_attention *h, int chunk_positions);
  * the reference; a measurement knob for the A/B of the matrix-core choice. */
 int leap_hip_attention_set_products(leap_hip_attention *h, int valu);
 
+/* How later steps finish a one-level split-K merge of 32 or more records
+ * (no counterpart in the reference: a device-side scheduling choice).
+ * 1 (the default): the second-to-last workgroup to count in waits for the
+ * last, polling its counter a bounded number of times, and the two fold
+ * half of the q heads each; 0: the last workgroup folds every head alone;
+ * 2: the waiting workgroup gives up at once, which exercises the fallback
+ * where the last folds every head.  All three give identical results.
+ * -EINVAL for other modes. */
+int leap_hip_attention_set_fold_helper(leap_hip_attention *h, int mode);
+
 /* Device addresses of the (seq, layer) cache slabs, for callers that keep
  * their own device-side views of the cache. */
 int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,

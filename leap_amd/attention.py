@@ -37,7 +37,7 @@ EXPORTS = (
     "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
     "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
     "leap_hip_attention_xcc_map", "leap_hip_attention_step_noalloc", "leap_hip_attention_floor_async",
-    "leap_hip_attention_set_products",
+    "leap_hip_attention_set_products", "leap_hip_attention_set_fold_helper",
 )
 
 PACKET_HEADER_BYTES = 8
@@ -115,6 +115,7 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_xcc_map.argtypes = [_I, _I, ctypes.POINTER(_I)]
     L.leap_hip_attention_floor_async.argtypes = [H, _I, _I, _I, _P, _I, ctypes.c_longlong, _P]
     L.leap_hip_attention_set_products.argtypes = [H, _I]
+    L.leap_hip_attention_set_fold_helper.argtypes = [H, _I]
     L.leap_hip_attention_step_noalloc.argtypes = [ctypes.POINTER(Config), _I] + [_P] * 8
     for name in EXPORTS:
         fn = getattr(L, name)
@@ -354,6 +355,12 @@ class HipAttention:
     def set_products(self, valu: bool):
         """Score and weighted-V products on the VALU (True) or the matrix cores."""
         self._check(self.lib.leap_hip_attention_set_products(self.h, 1 if valu else 0))
+
+    def set_fold_helper(self, mode: int):
+        """How a one-level merge's final fold is shared: 1 two workgroups (the
+        default), 0 the last workgroup alone, 2 the fallback path (the helper
+        gives up at once)."""
+        self._check(self.lib.leap_hip_attention_set_fold_helper(self.h, mode))
 
     def set_split(self, chunk_positions):
         self._check(self.lib.leap_hip_attention_set_split(self.h, chunk_positions))

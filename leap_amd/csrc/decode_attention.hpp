@@ -51,6 +51,9 @@ constexpr int kSubGroup = 8;              // chunks per first-level merge
 constexpr int kCtrStride = 32;            // ints between arrival counters: one 128-byte line each
 constexpr int kFinalMax = 40;            // records of a one-level fold (the asymmetric merge's 36 at 64 chunks)
 constexpr int kXcds = 8;                  // XCDs of an MI355X
+constexpr int kGiveUp = 1 << 20;          // added to a final counter by a fold helper that stopped waiting
+constexpr int kHelpPolls = 16384;         // a fold helper's polls of the final counter (a few ms)
+constexpr int kHelpMinRecords = 32;       // records from which two workgroups share a final fold
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
 
@@ -103,8 +106,9 @@ struct StepArgs {
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
     float scale_log2;    // log2(e) / sqrt(HD)
-    int merge_asym;      // every CU runs two one-pass workgroups of the launch: the
-                         // first-dispatched half of a group's chunks finishes first
+    int merge_asym;      // bit 0: every CU runs two workgroups of the launch, and the
+                         // first-dispatched half of a group's chunks finishes first;
+                         // bits 1-2: the fold helper (0 off, 1 on, 2 gives up at once)
     int spread_log2;     // a group's chunks are cut into 2^spread_log2 parts on as many
                          // XCDs (launches of fewer groups than XCDs); 0: one part
     int even_chunks;     // > 0: a sequence of T positions is cut instead into min(even_chunks, T)
@@ -337,6 +341,33 @@ struct Shape {
 // passes, for that rotation.  One-pass and long-run launches use PART =
 // false, whose prologue is shorter (the two measured 0.07-0.14 us apart per
 // launch at Llama-3-8B ctx 4096 and TinyLlama ctx 256).
+// The wait of the second-to-last arrival of a one-level fold that shares
+// the fold with the last arrival (one thread): poll the final counter, at
+// most kHelpPolls times (none in mode 2, which tests the fallback), until
+// the last arrival has counted in.  Returns 1 if this workgroup folds its
+// half of the heads, and then resets the counter.  On giving up it adds
+// kGiveUp to the counter: if the last arrival has counted in meanwhile
+// (the add returns target), it folds its half of the heads only and this
+// workgroup still folds the other half; otherwise the last arrival sees
+// kGiveUp, folds every head and resets the counter, and this returns 0.
+// Every head is folded once and the counter reset once, in any order.
+__device__ __forceinline__ int fold_helper_wait(int *ctr, int target, int mode)
+{
+    const int polls = mode == 2 ? 0 : kHelpPolls;
+    for (int i = 0; i < polls; i++) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target) {
+            *ctr = 0;
+            return 1;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (__hip_atomic_fetch_add(ctr, kGiveUp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) == target) {
+        *ctr = 0;
+        return 1;
+    }
+    return 0;
+}
+
 template <int HD, int G, int NW, bool MFMA = true, bool PART = false>
 __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(StepArgs a)
 {
@@ -830,26 +861,33 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
             mm = m_new;
         }
     };
-    // Fold records [first, first + n_rt), n_rt <= n, n <= MG * BW a
-    // compile-time count (std::integral_constant), as one batch of loads:
-    // record lane mg takes records mg, mg + MG, ..., and the lanes meet in
-    // LDS.  Leaves (ox, Mx, Lx) in the threads with mg == 0.  With n known,
-    // every load a lane issues is unconditional; records [n_rt, n) read past
-    // the range (0) and count as empty.  The (max, sum) pairs, which the D4
-    // lanes of a record lane all need, are loaded once per (head, record)
-    // across the workgroup, ahead of the partial outputs, and shared through
-    // LDS: a load of each pair in every lane that needs it cost about 0.5 us
-    // at Llama-3-8B ctx 4096.
-    auto fold_wide = [&](int first, auto n_c, int n_rt, float4 &ox, float &Mx, float &Lx) {
+    // Fold records [first, first + n_rt) of the heads [h0, h0 + GH) and emit
+    // the heads' results.  GH is a compile-time count: all GM heads, or half
+    // of them when two workgroups share the final fold.  The threads are
+    // laid out over those heads, with MGH record lanes per head: record lane
+    // fg takes records fg, fg + MGH, ... as one batch of loads (n <= MGH * BW
+    // a compile-time count, n_rt <= n; records [n_rt, n) read past the range,
+    // 0, and count as empty), and the lanes meet in LDS.  The (max, sum)
+    // pairs, which the D4 lanes of a record lane all need, are loaded once
+    // per (head, record) across the workgroup, ahead of the partial outputs,
+    // and shared through LDS: a load of each pair in every lane that needs it
+    // cost about 0.5 us at Llama-3-8B ctx 4096.
+    auto fold_emit = [&](int h0, auto gh_c, int first, auto n_c, int n_rt) {
+        constexpr int GH = decltype(gh_c)::value;
         constexpr int n = decltype(n_c)::value;
-        static_assert(n <= MG * BW && n <= kFinalMax, "records per lane");
-        constexpr int BL = (n + MG - 1) / MG;  // records per lane
-        constexpr int NML = GM * n;            // (head, record) pairs, padding heads included
+        constexpr int MGH = S::THREADS / (GH * D4);
+        static_assert(MGH * GH * D4 == S::THREADS, "fold layout");
+        static_assert(n <= MGH * BW && n <= kFinalMax, "records per lane");
+        const int fl = tid / (MGH * D4), fg = (tid / D4) % MGH, fd = tid % D4;  // head - h0, record lane, column
+        const int fh = h0 + fl;
+        const bool flive = fh < G;
+        constexpr int BL = (n + MGH - 1) / MGH;
+        constexpr int NML = GH * n;
         constexpr int MLT = (NML + S::THREADS - 1) / S::THREADS;
         float2 mlv[MLT];
 #pragma unroll
         for (int i = 0; i < MLT; i++) {
-            const int t = tid + i * S::THREADS, h = t / n, c = t % n;
+            const int t = tid + i * S::THREADS, h = h0 + t / n, c = t % n;
             const bool in = t < NML && h < G && c < n_rt;
             mlv[i] = buf_load2<kSc1>(wm_rsrc, in ? (uint32_t)(h * n_rec + first + c) * 8u : ws_ml_bytes);
         }
@@ -857,10 +895,10 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         float4 ob[BL];
 #pragma unroll
         for (int j = 0; j < BL; j++) {
-            const int c = mg + j * MG;
-            const uint32_t row = (uint32_t)(mh * n_rec + first + c);
-            const bool in = live && c < n_rt;
-            ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * md4 : ws_o_bytes);
+            const int c = fg + j * MGH;
+            const uint32_t row = (uint32_t)(fh * n_rec + first + c);
+            const bool in = flive && c < n_rt;
+            ob[j] = buf_load4<kSc1>(wo_rsrc, in ? row * (HD * 4u) + 16u * fd : ws_o_bytes);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -872,43 +910,42 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         float2 mlb[BL];
 #pragma unroll
         for (int j = 0; j < BL; j++) {
-            const int c = mg + j * MG;
-            mlb[j] = c < n ? ml_lds[mh * n + c] : make_float2(-INFINITY, 0.f);
+            const int c = fg + j * MGH;
+            mlb[j] = c < n ? ml_lds[fl * n + c] : make_float2(-INFINITY, 0.f);
         }
         float mm = -INFINITY, ll = 0.f;
         float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int j = 0; j < BL; j++)
-            if (mg + j * MG < n) mm = fmaxf(mm, mlb[j].x);
-        // a lane whose records are all empty keeps mm = -inf; its weights
-        // exp2(-inf - 0) are 0
+            if (fg + j * MGH < n) mm = fmaxf(mm, mlb[j].x);
         const float mref = (mm == -INFINITY) ? 0.f : mm;
 #pragma unroll
         for (int j = 0; j < BL; j++) {
-            const float w = (mg + j * MG < n) ? fast_exp2(mlb[j].x - mref) : 0.f;
+            const float w = (fg + j * MGH < n) ? fast_exp2(mlb[j].x - mref) : 0.f;
             fma4(oo, w, ob[j]);
             ll += w * mlb[j].y;
         }
         __syncthreads();  // LDS scratch is free
-        mo[(mh * MG + mg) * D4 + md4] = oo;
-        if (md4 == 0) {
-            mmx[mh * MG + mg] = mm;
-            mls[mh * MG + mg] = ll;
+        mo[(fl * MGH + fg) * D4 + fd] = oo;
+        if (fd == 0) {
+            mmx[fl * MGH + fg] = mm;
+            mls[fl * MGH + fg] = ll;
         }
         __syncthreads();
-        if (mg == 0) {
-            Mx = -INFINITY;
+        if (fg == 0 && flive) {
+            float Mx = -INFINITY;
 #pragma unroll
-            for (int g = 0; g < MG; g++) Mx = fmaxf(Mx, mmx[mh * MG + g]);
-            Lx = 0.f;
-            ox = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int g = 0; g < MGH; g++) Mx = fmaxf(Mx, mmx[fl * MGH + g]);
+            float Lx = 0.f;
+            float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int g = 0; g < MG; g++) {
-                const float mgv = mmx[mh * MG + g];
+            for (int g = 0; g < MGH; g++) {
+                const float mgv = mmx[fl * MGH + g];
                 const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
-                fma4(ox, sc, mo[(mh * MG + g) * D4 + md4]);
-                Lx += sc * mls[mh * MG + g];
+                fma4(ox, sc, mo[(fl * MGH + g) * D4 + fd]);
+                Lx += sc * mls[fl * MGH + g];
             }
+            emit(fh, fd, ox, Mx, Lx);
         }
     };
     // Fold records [first, first + n) of the G heads into (ox, Mx, Lx) of
@@ -952,6 +989,41 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     };
     int *ctr = a.counters + (size_t)pgroup * (size_t)counters_per_group(a.grid_chunks);
 
+    // The fold of a one-level merge's records [first, first + n_rt) (n_c a
+    // compile-time bound), after this workgroup counted in with result prev.
+    // The last arrival folds.  From kHelpMinRecords records on (G > 1) the
+    // heads are folded in two halves, and with the helper on (a.merge_asym
+    // >> 1) the second-to-last arrival waits for the last (fold_helper_wait)
+    // and folds the second half: that halves the bytes the last arrival's CU
+    // takes in, and a fold's time grows by about 24 ns per 2 KiB record at
+    // Llama-3-8B.
+    auto final_fold = [&](int first, auto n_c, int n_rt, int prev) {
+        if constexpr (GM >= 2) {
+            if (n_rt >= kHelpMinRecords) {
+                // The two halves of the heads are folded with the same
+                // layout whoever folds them, so the result does not depend
+                // on the helper.
+                constexpr auto gh = std::integral_constant<int, GM / 2>{};
+                const int help = a.merge_asym >> 1;
+                if (help && prev == n_rt - 2) {
+                    __syncthreads();  // every thread has read s_last
+                    if (tid == 0) s_last = fold_helper_wait(ctr, n_rt, help);
+                    __syncthreads();
+                    if (s_last) fold_emit(GM / 2, gh, first, n_c, n_rt);
+                    return;
+                }
+                if ((prev & (kGiveUp - 1)) != n_rt - 1) return;
+                fold_emit(0, gh, first, n_c, n_rt);
+                if (help && prev < kGiveUp) return;  // the helper folds the other half
+                if (tid == 0) ctr[0] = 0;
+                fold_emit(GM / 2, gh, first, n_c, n_rt);
+                return;
+            }
+        }
+        if ((prev & (kGiveUp - 1)) != n_rt - 1) return;
+        if (tid == 0) ctr[0] = 0;
+        fold_emit(0, std::integral_constant<int, GM>{}, first, n_c, n_rt);
+    };
     // The asymmetric merge (see the header), for NC chunks: chunks [0, NC/2)
     // fold in sub-groups whose records go right after the chunk records, and
     // the final fold reads records [NC/2, NC + NC/2/kSubGroup), one range.
@@ -982,17 +1054,10 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) {
-            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            s_last = (prev == n_final - 1);
-        }
+        if (tid == 0) s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         __syncthreads();
-        if (!s_last) return;
-        if (tid == 0) ctr[0] = 0;
-        float4 of;
-        float Mf, Lf;
-        fold_wide(half, std::integral_constant<int, n_final>{}, n_final, of, Mf, Lf);
-        if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
+        const int prev = s_last;
+        final_fold(half, std::integral_constant<int, n_final>{}, n_final, prev);
     };
     // One level for launches without the asymmetric shape and 2-40 chunks:
     // every chunk counts into the final counter and the last folds all
@@ -1007,19 +1072,12 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
         constexpr int NC = decltype(nc_c)::value;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) {
-            const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            s_last = (prev == n_local - 1);
-        }
+        if (tid == 0) s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         __syncthreads();
-        if (!s_last) return;
-        if (tid == 0) ctr[0] = 0;
-        float4 of;
-        float Mf, Lf;
-        fold_wide(0, std::integral_constant<int, NC>{}, n_local, of, Mf, Lf);
-        if (mg == 0 && live) emit(mh, md4, of, Mf, Lf);
+        const int prev = s_last;
+        final_fold(0, std::integral_constant<int, NC>{}, n_local, prev);
     };
-    if (!a.merge_asym && n_local > 1) {
+    if (!(a.merge_asym & 1) && n_local > 1) {
         if (n_local <= 8) return merge_flat(std::integral_constant<int, 8>{});
         if constexpr (16 <= MG * BW) {
             if (n_local <= 16) return merge_flat(std::integral_constant<int, 16>{});
@@ -1034,7 +1092,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
             if (n_local <= 40) return merge_flat(std::integral_constant<int, 40>{});
         }
     }
-    if (a.merge_asym) {
+    if (a.merge_asym & 1) {
         if constexpr (32 + 4 <= MG * BW) {
             if (n_local == 64) return merge_asym(std::integral_constant<int, 64>{});
         }

@@ -77,6 +77,7 @@ struct leap_hip_attention {
     int n_cu = 256;  // compute units of the device
     int max_chunks = 1;  // chunks per sequence the workspace holds records for
     bool valu = false;   // score and weighted-V products on the VALU (measurement knob)
+    int fold_helper = 1; // 1: two workgroups share a one-level merge's final fold; 0: the last alone; 2: test of the fallback
     std::string err;
 };
 
@@ -176,6 +177,7 @@ struct LaunchShape {
     int max_chunks;
     bool valu = false;  // products as VALU FMAs instead of MFMAs (the A/B knob)
     bool ws_parts = true;  // the buffers hold part records and kXcds part-groups' records
+    int fold_helper = 1;   // leap_hip_attention_set_fold_helper
 };
 
 // The device buffers of one launch (one layer): the cache slabs of sequence
@@ -195,8 +197,10 @@ struct LaunchBuffers {
 
 LaunchShape shape_of(const leap_hip_attention *h)
 {
-    return LaunchShape{h->cfg.head_dim, h->group, h->cfg.n_heads, h->cfg.n_kv_heads, h->cfg.seq_len,
-                       h->n_cu, h->split, h->max_chunks, h->valu};
+    LaunchShape s{h->cfg.head_dim, h->group, h->cfg.n_heads, h->cfg.n_kv_heads, h->cfg.seq_len,
+                  h->n_cu, h->split, h->max_chunks, h->valu};
+    s.fold_helper = h->fold_helper;
+    return s;
 }
 
 // Positions per workgroup (chunk), from the size and shape of the launch:
@@ -416,8 +420,9 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     // streams.  Chunks of 2-8 passes at Llama-3-8B, against the two-level
     // tree: ctx 4608 13.48 -> 12.78 us, 8192 16.41 -> 15.86, 16384 25.57 ->
     // 25.04 us.
-    a.merge_asym = (chunk <= 8 * leap::rows_per_pass(hd, s.group, kWaves) &&
-                    n_pgroups * grid_x >= 2LL * launch_cus(s, n_seq, total_rows)) ? 1 : 0;
+    const int asym = (chunk <= 8 * leap::rows_per_pass(hd, s.group, kWaves) &&
+                      n_pgroups * grid_x >= 2LL * launch_cus(s, n_seq, total_rows)) ? 1 : 0;
+    a.merge_asym = asym | (s.fold_helper << 1);
     hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
     MergeFn mf = pick_merge(hd, s.group);
@@ -1361,6 +1366,14 @@ int leap_hip_attention_set_products(leap_hip_attention *h, int valu)
     if (!h) return -EINVAL;
     if (valu != 0 && valu != 1) return set_err(h, -EINVAL, "products mode %d is not 0 (MFMA) or 1 (VALU)", valu);
     h->valu = valu == 1;
+    return 0;
+}
+
+int leap_hip_attention_set_fold_helper(leap_hip_attention *h, int mode)
+{
+    if (!h) return -EINVAL;
+    if (mode < 0 || mode > 2) return set_err(h, -EINVAL, "fold helper mode %d is not 0, 1 or 2", mode);
+    h->fold_helper = mode;
     return 0;
 }
 

@@ -74,6 +74,7 @@ def test_null_arguments():
     assert lib.leap_hip_attention_kv_upload(None, 0, 0, 0, 1, None, None) == -errno.EINVAL
     assert lib.leap_hip_attention_set_split(None, 64) == -errno.EINVAL
     assert lib.leap_hip_attention_set_products(None, 1) == -errno.EINVAL
+    assert lib.leap_hip_attention_set_fold_helper(None, 1) == -errno.EINVAL
     assert lib.leap_hip_attention_floor_async(None, 1, 0, 1, None, 0, 1, None) == -errno.EINVAL
 
 

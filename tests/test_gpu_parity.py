@@ -475,3 +475,36 @@ def test_spread_ragged_batch_with_empty_parts():
             assert_close(out[s], want, what=f"sequence {s}")
             kr, vr = att.kv_download(s, 0, T - 1, T)
             assert np.array_equal(kr[0], orc.key_cache[0, T - 1]) and np.array_equal(vr[0], orc.value_cache[0, T - 1])
+
+
+# ---- the final fold shared by two workgroups --------------------------------------
+
+@pytest.mark.parametrize("nh,nkv,hd,T", [
+    (32, 8, 128, 4096),   # the asymmetric merge, 36 records
+    (32, 8, 128, 2048),   # one level, 32 records
+    (32, 8, 128, 1984),   # one level, 31 of 32 compiled records
+    (24, 8, 128, 3000),   # three q heads per KV head (a padding head in the second half)
+    (32, 4, 64, 1500),    # head_dim 64, eight q heads per KV head
+    (64, 8, 128, 2048),   # eight q heads at head_dim 128 (a two-level tree: no shared fold)
+    (16, 2, 128, 2048),   # two q heads per KV head
+])
+def test_fold_helper_modes_agree(nh, nkv, hd, T):
+    """The final fold shared by the last two arrivals (mode 1), done by the
+    last alone (0), and the fallback where the waiting workgroup gives up at
+    once (2) give bitwise equal outputs, step after step (every mode leaves
+    the arrival counters at zero), and meet the oracle."""
+    theta = 10000.0 if hd == 64 else 500000.0
+    rng = rng_for(301, nh, nkv, hd, T)
+    pos = T - 1
+    q, k, v = normal(rng, nh * hd, hd), normal(rng, nkv * hd, hd), normal(rng, nkv * hd, hd)
+    outs = []
+    with HipAttention(nh, nkv, hd, T, rope_theta=theta) as att:
+        att.kv_fill_normal(0x4C454150 + 301, 1.0 / np.sqrt(hd))
+        for mode in (1, 0, 2, 1, 2, 0, 1):
+            att.set_fold_helper(mode)
+            outs.append(att.step(0, pos, q, k, v))
+        _step_and_check(att, 0, pos, q, k, v, theta, out=outs[0])
+        with pytest.raises(LeapError):
+            att.set_fold_helper(3)
+    for i, o in enumerate(outs[1:], 1):
+        assert np.array_equal(o, outs[0]), f"step {i} differs from the first"
