@@ -62,7 +62,7 @@ typedef struct leap_hip_attention_config {
     int layer_begin; /* first layer held by this handle                        */
     int layer_end;   /* one past the last layer held                           */
     int n_heads;     /* query heads                                            */
-    int n_kv_heads;  /* key/value heads; n_heads % n_kv_heads == 0             */
+    int n_kv_heads;  /* key/value heads; n_heads / n_kv_heads in {1,2,3,4,8,16} */
     int head_dim;    /* dim / n_heads: 64 or 128                               */
     int seq_len;     /* cache rows per layer (Config.seq_len)                  */
     float rope_theta;/* 500000 in the reference; <= 0 selects 500000           */

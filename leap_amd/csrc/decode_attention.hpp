@@ -101,7 +101,7 @@ struct StepArgs {
     int max_pos;         // launch was sized for positions <= max_pos
     int seq_len;
     int n_heads;
-    int n_kv_heads;
+    int n_kv_heads;      // KV groups per sequence (with kv_split, twice the cache's KV heads)
     int chunk;           // positions per workgroup, a multiple of 8 (passes past its end are masked)
     int grid_chunks;     // chunks per sequence in the launch grid
     int n_groups;        // n_seq * n_kv_heads
@@ -117,7 +117,26 @@ struct StepArgs {
                          // prologue reads first keep their offsets
     float *ws_po;        // [n_groups << spread_log2][G][HD] each part's unnormalised output
     float2 *ws_pml;      // [n_groups << spread_log2][G] its (max, sum), log2 units
+    int kv_split;        // 1: n_kv_heads counts each of the cache's n_kv_heads / 2 heads twice, as
+                         // two groups of G q heads (kv_group); 0: one group per head
 };
+
+// The cache's KV head and the first q head of a launch's KV group kvv (of
+// n_kv_heads).  With kv_split, the cache holds n_kv = n_kv_heads / 2 heads of
+// 2G q heads each, served as two groups of G: half 0 is groups [0, n_kv),
+// half 1 groups [n_kv, 2 n_kv), so that with n_kv a multiple of 8 both halves
+// of a head run on one XCD and the second read of its rows can hit in L2.
+struct KvGroup {
+    int kvh, half, qh0;
+};
+template <int G>
+__device__ __forceinline__ KvGroup kv_group(int kvv, int n_kv_heads, int kv_split)
+{
+    const int n_kv = n_kv_heads >> kv_split;
+    const int half = kvv >= n_kv ? 1 : 0;
+    const int kvh = kvv - half * n_kv;
+    return KvGroup{kvh, half, ((kvh << kv_split) + half) * G};
+}
 
 // Whether a launch runs the PART instance of the decode kernel (the host's
 // choice, restated for the floor kernels, which have no such instance):
@@ -368,7 +387,7 @@ __device__ __forceinline__ int fold_helper_wait(int *ctr, int target, int mode)
     return 0;
 }
 
-template <int HD, int G, int NW, bool MFMA = true, bool PART = false>
+template <int HD, int G, int NW, bool MFMA = true, bool PART = false, bool KVS = false>
 __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(StepArgs a)
 {
     using S = Shape<HD, G, NW>;
@@ -396,7 +415,12 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     const int part = pgroup & ((1 << a.spread_log2) - 1);
     const int chunk_id = part * a.grid_chunks + lc;  // within the group
     const int seq = group / a.n_kv_heads;
-    const int kvh = group % a.n_kv_heads;
+    // KVS: two launch groups per cache head (kv_split set), compiled as
+    // instances of their own so that the others keep their code
+    const KvGroup kg = KVS ? kv_group<G>(group % a.n_kv_heads, a.n_kv_heads, 1)
+                           : KvGroup{group % a.n_kv_heads, 0, (group % a.n_kv_heads) * G};
+    const int kvh = kg.kvh;
+    const bool store_new = kg.half == 0;  // the one group per cache head that appends the new token
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
@@ -409,7 +433,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     // chunks of this part (at least 1 here)
     const int n_local = min(a.grid_chunks, n_chunks - part * a.grid_chunks);
 
-    const int kv_dim = a.n_kv_heads * HD;
+    const int kv_dim = (KVS ? a.n_kv_heads / 2 : a.n_kv_heads) * HD;
     const int q_dim = a.n_heads * HD;
     const uint32_t row_bytes = (uint32_t)kv_dim * 4u;
     const size_t slab = (size_t)seq * (size_t)a.seq_stride;
@@ -435,7 +459,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)row_end * row_bytes);
     const float *k_row_new = a.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
     const float *v_row_new = a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
-    const float *qg = a.q + (size_t)seq * q_dim + (size_t)kvh * G * HD;
+    const float *qg = a.q + (size_t)seq * q_dim + (size_t)kg.qh0 * HD;
     const float4 *rope_row = a.rope + (size_t)pos * (HD / 4);
 
     __shared__ __align__(16) float p_lds[NW][R * G];
@@ -615,7 +639,8 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 #pragma unroll
                     for (int f = 0; f < NF; f++) {
                         kb[ks][f] = rope4(knew[f], tab[f]);
-                        *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = kb[ks][f];
+                        if (store_new)
+                            *reinterpret_cast<float4 *>(kc + (size_t)t * kv_dim + 4 * (8 * f + ksl)) = kb[ks][f];
                     }
                 }
             }
@@ -722,7 +747,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
                 const float4 vnew = lane_float4(vnew_l, vj);
                 if (base + r == pos) {
                     vb[vs] = vnew;
-                    *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
+                    if (store_new) *reinterpret_cast<float4 *>(vc + (size_t)(base + r) * kv_dim + 4 * vj) = vnew;
                 }
             }
 #pragma unroll
@@ -779,7 +804,7 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
             if (col == 0) a.ws_pml[(size_t)pgroup * G + head] = make_float2(M, L);
         } else {
             scale4(o, 1.0f / L);
-            reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + head) * HD)[col] = o;
+            reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kg.qh0 + head) * HD)[col] = o;
         }
     };
     const uint32_t ws_o_bytes = (uint32_t)(G * n_rec * HD) * 4u;
@@ -1157,10 +1182,11 @@ __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
     // the argument block as one batch of loads, as in the decode kernel
     asm volatile("" ::"s"(a.pos_dev), "s"(a.ws_po), "s"(a.ws_pml), "s"(a.out), "s"(a.pos_scalar), "s"(a.max_pos),
                  "s"(a.seq_len), "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
-                 "s"(a.n_groups), "s"(a.spread_log2), "s"(a.even_chunks));
+                 "s"(a.n_groups), "s"(a.spread_log2), "s"(a.even_chunks), "s"(a.kv_split));
     const int group = blockIdx.x;
     if (group >= a.n_groups) return;
-    const int seq = group / a.n_kv_heads, kvh = group % a.n_kv_heads;
+    const int seq = group / a.n_kv_heads;
+    const KvGroup kg = kv_group<G>(group % a.n_kv_heads, a.n_kv_heads, a.kv_split);
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
     const int n_chunks = seq_chunks(a, pos + 1);
@@ -1179,7 +1205,7 @@ __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
     }
     scale4(o, 1.0f / L);
     const int q_dim = a.n_heads * HD;
-    reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kvh * G + h) * HD)[c] = o;
+    reinterpret_cast<float4 *>(a.out + (size_t)seq * q_dim + (size_t)(kg.qh0 + h) * HD)[c] = o;
 }
 
 // ---- launch and stream floors (measurement only) ----------------------------
@@ -1208,21 +1234,21 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
     // the argument block as one batch of loads, as in the decode kernel
     asm volatile("" ::"s"(a.k_cache), "s"(a.v_cache), "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar),
                  "s"(a.max_pos), "s"(a.seq_len), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
-                 "s"(a.n_groups), "s"(a.even_chunks));
+                 "s"(a.n_groups), "s"(a.even_chunks), "s"(a.kv_split));
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
     const int chunk_id = local % a.grid_chunks;
     const int group = (local / a.grid_chunks) * kXcds + xcd;
     if (group >= a.n_groups) return;
     const int seq = group / a.n_kv_heads;
-    const int kvh = group % a.n_kv_heads;
+    const int kvh = kv_group<G>(group % a.n_kv_heads, a.n_kv_heads, a.kv_split).kvh;
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
     const int T = pos + 1;
     const int n_chunks = seq_chunks(a, T);
     if (chunk_id >= n_chunks) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t row_bytes = (uint32_t)(a.n_kv_heads * HD) * 4u;
+    const uint32_t row_bytes = (uint32_t)((a.n_kv_heads >> a.kv_split) * HD) * 4u;
     const size_t slab = (size_t)seq * (size_t)a.seq_stride;
     const int chunk_begin = chunk_start(a, T, n_chunks, chunk_id);
     const int chunk_end = chunk_start(a, T, n_chunks, chunk_id + 1);

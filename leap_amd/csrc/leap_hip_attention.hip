@@ -141,20 +141,49 @@ enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
 
 // part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
 // long (leap::part_launch).
-KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false, bool part = false)
+// kvs: two launch groups of g heads per cache head (kv_split; g = 8 only).
+KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false, bool part = false, bool kvs = false)
 {
 #define LEAP_CASE(HD, G)                                                                                   \
-    if (hd == HD && g == G)                                                                                \
+    if (hd == HD && g == G && !kvs)                                                                        \
         return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>                           \
                : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>                           \
                : part ? (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, true>                  \
                               : leap::decode_attention_kernel<HD, G, kWaves, true, true>)                  \
                       : (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, false>                 \
                               : leap::decode_attention_kernel<HD, G, kWaves, true, false>);
+#define LEAP_CASE_KVS(HD)                                                                                  \
+    if (hd == HD && g == 8 && kvs)                                                                         \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, 8, kWaves>                           \
+               : kind == kFloorStream ? leap::floor_stream_kernel<HD, 8, kWaves>                           \
+               : part ? (valu ? leap::decode_attention_kernel<HD, 8, kWaves, false, true, true>            \
+                              : leap::decode_attention_kernel<HD, 8, kWaves, true, true, true>)            \
+                      : (valu ? leap::decode_attention_kernel<HD, 8, kWaves, false, false, true>           \
+                              : leap::decode_attention_kernel<HD, 8, kWaves, true, false, true>);
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+    LEAP_CASE_KVS(64) LEAP_CASE_KVS(128)
 #undef LEAP_CASE
+#undef LEAP_CASE_KVS
     return nullptr;
+}
+
+// How launches see a head shape: 16 q heads per KV head run as two groups
+// of 8 per cache head (the decode kernel's kv_split), so that no kernel
+// instance holds more than 8 heads' accumulators; other shapes as they are.
+struct KvView {
+    int group;       // q heads per launch group
+    int n_kv_heads;  // launch groups per sequence
+    int kv_split;
+};
+KvView kv_view(int group, int n_kv_heads)
+{
+    return group == 16 ? KvView{8, 2 * n_kv_heads, 1} : KvView{group, n_kv_heads, 0};
+}
+bool shape_supported(int head_dim, int group)
+{
+    const KvView v = kv_view(group, 1);
+    return pick_kernel(head_dim, v.group, kDecode, false, false, v.kv_split != 0) != nullptr;
 }
 
 int check_layer(leap_hip_attention *h, int layer)
@@ -178,6 +207,7 @@ struct LaunchShape {
     bool valu = false;  // products as VALU FMAs instead of MFMAs (the A/B knob)
     bool ws_parts = true;  // the buffers hold part records and kXcds part-groups' records
     int fold_helper = 1;   // leap_hip_attention_set_fold_helper
+    int kv_split = 0;      // group and n_kv_heads are kv_view's (two launch groups per cache head)
 };
 
 // The device buffers of one launch (one layer): the cache slabs of sequence
@@ -197,9 +227,11 @@ struct LaunchBuffers {
 
 LaunchShape shape_of(const leap_hip_attention *h)
 {
-    LaunchShape s{h->cfg.head_dim, h->group, h->cfg.n_heads, h->cfg.n_kv_heads, h->cfg.seq_len,
+    const KvView v = kv_view(h->group, h->cfg.n_kv_heads);
+    LaunchShape s{h->cfg.head_dim, v.group, h->cfg.n_heads, v.n_kv_heads, h->cfg.seq_len,
                   h->n_cu, h->split, h->max_chunks, h->valu};
     s.fold_helper = h->fold_helper;
+    s.kv_split = v.kv_split;
     return s;
 }
 
@@ -369,7 +401,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     // The PART instance: chunks that are not whole passes, and chunks of 2-8
     // passes, whose pass order it rotates.
     const bool part = leap::part_launch(even, chunk, leap::rows_per_pass(hd, s.group, kWaves));
-    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part);
+    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split != 0);
     if (!fn) return hipErrorInvalidValue;
     const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
     if (n_chunk_max > s.max_chunks) return hipErrorInvalidValue;
@@ -404,6 +436,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
 
     a.spread_log2 = spread_log2;
+    a.kv_split = s.kv_split;
     a.ws_po = b.ws_po;
     a.ws_pml = b.ws_pml;
 
@@ -434,7 +467,7 @@ int launch(leap_hip_attention *h, int layer, int n_seq, const int *pos_dev, int 
            int max_pos, long long total_rows, const float *q, const float *k, const float *v,
            float *out, hipStream_t stream, int kind = kDecode)
 {
-    if (!pick_kernel(h->cfg.head_dim, h->group))
+    if (!shape_supported(h->cfg.head_dim, h->group))
         return set_err(h, -EINVAL, "unsupported head_dim %d / group %d", h->cfg.head_dim, h->group);
     const size_t loff = (size_t)(layer - h->cfg.layer_begin) * h->layer_floats;
     const LaunchBuffers b{h->k_cache + loff, h->v_cache + loff, (long long)h->slab_floats, h->rope,
@@ -677,7 +710,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     if (c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_heads % c.n_kv_heads != 0)
         return set_err(nullptr, -EINVAL, "n_heads %d must be a positive multiple of n_kv_heads %d",
                        c.n_heads, c.n_kv_heads);
-    if (!pick_kernel(c.head_dim, c.n_heads / c.n_kv_heads))
+    if (!shape_supported(c.head_dim, c.n_heads / c.n_kv_heads))
         return set_err(nullptr, -EINVAL, "unsupported head_dim %d with %d q heads per kv head",
                        c.head_dim, c.n_heads / c.n_kv_heads);
     if (c.seq_len <= 0 || c.n_layers <= 0 || c.layer_begin < 0 || c.layer_end > c.n_layers ||
@@ -750,11 +783,13 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMemcpyAsync(h->rope, packed.data(), packed.size() * sizeof(float),
                               hipMemcpyHostToDevice, h->stream));
 
-    h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, h->group, c.n_kv_heads, h->n_cu, leap::kMaxChunks);
-    // records and counters for max_batch * n_kv_heads groups, or for kXcds
-    // part-groups when a launch spreads fewer groups over the XCDs
-    const size_t n_pg = std::max<size_t>((size_t)c.max_batch * c.n_kv_heads, leap::kXcds);
-    const size_t ws_rows = n_pg * h->group * leap::records_per_head(h->max_chunks);
+    // launch groups (kv_view), their records and counters: for max_batch *
+    // n_kv_heads groups, or for kXcds part-groups when a launch spreads fewer
+    // groups over the XCDs
+    const KvView kvv = kv_view(h->group, c.n_kv_heads);
+    h->max_chunks = max_chunks_for(c.seq_len, c.head_dim, kvv.group, kvv.n_kv_heads, h->n_cu, leap::kMaxChunks);
+    const size_t n_pg = std::max<size_t>((size_t)c.max_batch * kvv.n_kv_heads, leap::kXcds);
+    const size_t ws_rows = n_pg * kvv.group * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
     h->counter_bytes = n_pg * leap::counters_per_group(h->max_chunks) * sizeof(int);
@@ -862,9 +897,11 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 // (max, sum) records, then its partial outputs, each 256-byte aligned.
 void scratch_layout(const leap_hip_attention_config &c, size_t *ml_off, size_t *o_off, size_t *total)
 {
-    // records for n_kv_heads groups, or for kXcds part-groups of a spread launch
-    const size_t n_pg = std::max<size_t>((size_t)c.n_kv_heads, leap::kXcds);
-    const size_t rec = n_pg * (size_t)(c.n_heads / c.n_kv_heads) * leap::records_per_head(kScratchChunks);
+    // records for the launch groups (kv_view), or for kXcds part-groups of a
+    // spread launch
+    const KvView v = kv_view(c.n_heads / c.n_kv_heads, c.n_kv_heads);
+    const size_t n_pg = std::max<size_t>((size_t)v.n_kv_heads, leap::kXcds);
+    const size_t rec = n_pg * (size_t)v.group * leap::records_per_head(kScratchChunks);
     *ml_off = align256(kScratchCounterBytes) + align256(kScratchPartOBytes) + align256(kScratchPartMlBytes);
     *o_off = *ml_off + align256(rec * sizeof(float2));
     *total = *o_off + rec * (size_t)c.head_dim * sizeof(float);
@@ -892,12 +929,13 @@ int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int po
         return set_err(nullptr, -EINVAL, "n_heads %d must be a positive multiple of n_kv_heads %d", c.n_heads,
                        c.n_kv_heads);
     const int group = c.n_heads / c.n_kv_heads;
-    if (!pick_kernel(c.head_dim, group))
+    if (!shape_supported(c.head_dim, group))
         return set_err(nullptr, -EINVAL, "unsupported head_dim %d with %d q heads per kv head", c.head_dim, group);
+    const KvView kvv = kv_view(group, c.n_kv_heads);
     if (c.seq_len <= 0) return set_err(nullptr, -EINVAL, "seq_len %d", c.seq_len);
-    if (c.n_kv_heads > kScratchMaxKvHeads)
-        return set_err(nullptr, -EINVAL, "%d kv heads: the static workspace holds counters for %d", c.n_kv_heads,
-                       kScratchMaxKvHeads);
+    if (kvv.n_kv_heads > kScratchMaxKvHeads)
+        return set_err(nullptr, -EINVAL, "%d kv groups: the static workspace holds counters for %d",
+                       kvv.n_kv_heads, kScratchMaxKvHeads);
     const unsigned long long slab_bytes = ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, 1, kWaves)) *
                                           (unsigned long long)c.n_kv_heads * c.head_dim * sizeof(float);
     if (slab_bytes >= (1ull << 32))
@@ -938,7 +976,8 @@ int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int po
         d.ptr = static_cast<unsigned char *>(p);
     });
     if (d.rc) return set_err(nullptr, d.rc, "%s", d.msg);
-    const LaunchShape shape{c.head_dim, group, c.n_heads, c.n_kv_heads, c.seq_len, d.n_cu, 0, kScratchChunks};
+    LaunchShape shape{c.head_dim, kvv.group, c.n_heads, kvv.n_kv_heads, c.seq_len, d.n_cu, 0, kScratchChunks};
+    shape.kv_split = kvv.kv_split;
     const size_t po_off = align256(kScratchCounterBytes), pml_off = po_off + align256(kScratchPartOBytes);
     const LaunchBuffers b{k_cache,
                           v_cache,

@@ -46,7 +46,8 @@ def _create(**kw):
     (dict(n_kv_heads=3), "multiple"),
     (dict(n_heads=0), "multiple"),
     (dict(head_dim=96), "head_dim"),
-    (dict(head_dim=128, n_heads=32, n_kv_heads=2), "head_dim"),  # 16 q heads per kv head
+    (dict(head_dim=128, n_heads=32, n_kv_heads=1), "head_dim"),  # 32 q heads per kv head
+    (dict(head_dim=128, n_heads=24, n_kv_heads=4), "head_dim"),  # 6 q heads per kv head
     (dict(layer_begin=1, layer_end=1), "layer range"),
     (dict(layer_end=3), "layer range"),
     (dict(seq_len=0), "seq_len"),

@@ -76,6 +76,7 @@ def test_reference_golden_fixtures():
 SHAPES = [  # n_heads, n_kv_heads, head_dim
     (32, 4, 64), (32, 8, 128), (64, 8, 128), (8, 8, 128), (16, 2, 128), (8, 4, 64), (4, 4, 64),
     (16, 16, 64), (8, 2, 64), (24, 8, 128), (12, 4, 64),  # kv_mul 3: Llama-3.2-3B's 24/8 at head_dim 128
+    (128, 8, 128), (32, 2, 64),  # kv_mul 16 (Llama-3.1-405B's 128/8 at head_dim 128): two groups of 8 per KV head
 ]
 
 
@@ -222,6 +223,28 @@ def test_batched_ragged_llama3_8b():
         out = att.step_batched(5, Ts - 1, q, k, v)
         for i in range(S):
             _step_and_check(att, 5, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+
+
+def test_llama31_405b_heads_ragged_batch():
+    """16 q heads per KV head (Llama-3.1-405B's 128/8/128), run as two groups
+    of 8 per KV head: a ragged batch of 6 sequences over every launch regime,
+    each sequence's output and appended cache row against the oracle."""
+    nh, nkv, hd, S = 128, 8, 128, 6
+    Ts = np.array([1, 65, 700, 3000, 4096, 9000])
+    rng = rng_for(405, S)
+    with HipAttention(nh, nkv, hd, 9000, n_layers=2, max_batch=S) as att:
+        att.kv_fill_normal(0x4C454150 + 405, 1.0 / np.sqrt(hd))
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(1, Ts - 1, q, k, v)
+        for i in range(S):
+            _step_and_check(att, 1, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
+        # one sequence at a time: the launch shapes of batch 1 (two workgroups
+        # per CU, near-equal chunks, the asymmetric merge at 4096)
+        for i in (3, 4, 5):
+            o1 = att.step(1, int(Ts[i]) - 1, q[i], k[i], v[i])
+            _step_and_check(att, 1, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=0, out=o1)
 
 
 @pytest.mark.parametrize("split", [64, 24])

@@ -40,7 +40,8 @@ def _rotated_row(att, pos, k_new):
 # that spreads each group over several XCDs and merges the parts in a second
 # launch)
 MEAN_SHAPES = [(32, 8, 128, 131072, 500000.0), (32, 8, 128, 4096, 500000.0), (32, 4, 64, 256, 10000.0),
-               (8, 1, 128, 32768, 500000.0), (64, 8, 128, 8192, 500000.0)]
+               (8, 1, 128, 32768, 500000.0), (64, 8, 128, 8192, 500000.0),
+               (128, 8, 128, 8192, 500000.0)]  # Llama-3.1-405B heads: 16 q heads per KV head
 
 
 @pytest.mark.parametrize("nh,nkv,hd,T,theta", MEAN_SHAPES)
@@ -78,7 +79,9 @@ def test_permuting_cached_positions_leaves_output_unchanged(nh, nkv, hd, T):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,T", [(32, 8, 128, 4096), (24, 8, 128, 4096), (64, 8, 128, 8192),
-                                         (16, 8, 64, 300), (32, 4, 64, 256)])
+                                         (16, 8, 64, 300), (32, 4, 64, 256),
+                                         # 16 q heads per KV head, run as two groups of 8
+                                         (128, 8, 128, 4096), (128, 8, 128, 300), (32, 2, 64, 2000)])
 def test_gqa_heads_with_equal_q_give_identical_outputs(nh, nkv, hd, T):
     rng = rng_for(203, nh, nkv, hd, T)
     g = nh // nkv
