@@ -383,7 +383,7 @@ def _random_cases(n, seed):
     """Seeded draws over the supported space: head shape, context, forced
     chunk size (0 = the automatic choice) and batch with ragged positions."""
     shapes = [(32, 8, 128), (24, 8, 128), (16, 16, 64), (32, 4, 64), (64, 8, 128), (8, 8, 128),
-              (16, 2, 128), (12, 4, 64), (8, 1, 64), (4, 2, 64)]
+              (16, 2, 128), (12, 4, 64), (8, 1, 64), (4, 2, 64), (128, 8, 128), (16, 1, 64)]
     rng = np.random.default_rng(seed)
     for i in range(n):
         nh, nkv, hd = shapes[rng.integers(len(shapes))]
@@ -417,7 +417,7 @@ def _random_cases_long(n, seed):
     launches of few KV heads, forced chunk sizes that are not whole passes,
     and batches of near-equal lengths (cut into near-equal chunks too)."""
     shapes = [(32, 8, 128), (24, 8, 128), (16, 16, 64), (32, 4, 64), (64, 8, 128), (8, 8, 128),
-              (16, 2, 128), (12, 4, 64), (8, 1, 64), (8, 1, 128), (32, 4, 128)]
+              (16, 2, 128), (12, 4, 64), (8, 1, 64), (8, 1, 128), (32, 4, 128), (128, 8, 128), (16, 1, 128)]
     rng = np.random.default_rng(seed)
     for i in range(n):
         nh, nkv, hd = shapes[rng.integers(len(shapes))]
