@@ -94,6 +94,8 @@ WORKLOADS = {
     "llama3-8b-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 5),
     "llama3-8b-q8-block-ctx4096": (32, 32, 8, 128, 500000.0, 1, 4096, 6),
     "llama3.2-3b-ctx4096": (28, 24, 8, 128, 500000.0, 1, 4096, 7),
+    # a pipeline stage of Llama-3.1-405B (16 of its 126 layers): 16 q heads per KV head
+    "llama3.1-405b-stage16-ctx4096": (16, 128, 8, 128, 500000.0, 1, 4096, 8),
 }
 SHAPE_NAMES = {
     "llama3-8b-ctx4096": "Llama-3-8B shape ctx 4096",
@@ -104,13 +106,15 @@ SHAPE_NAMES = {
     "llama3-8b-block-ctx4096": "Llama-3-8B ctx 4096",
     "llama3-8b-q8-block-ctx4096": "Llama-3-8B ctx 4096",
     "llama3.2-3b-ctx4096": "Llama-3.2-3B shape (24/8/128) ctx 4096",
+    "llama3.1-405b-stage16-ctx4096": "Llama-3.1-405B stage (128/8/128, 16 layers) ctx 4096",
 }
 BLOCK_WORKLOADS = {"llama3-8b-block-ctx4096", "llama3-8b-q8-block-ctx4096"}
 Q8_WORKLOADS = {"llama3-8b-q8-block-ctx4096"}
 DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3-8b-batch64-ragged": 10, "llama3-70b-stage20-batch16": 10,
                  "llama3.1-8b-ctx131072": 10, "llama3-8b-block-ctx4096": 30,
-                 "llama3-8b-q8-block-ctx4096": 50, "llama3.2-3b-ctx4096": 100}
+                 "llama3-8b-q8-block-ctx4096": 50, "llama3.2-3b-ctx4096": 100,
+                 "llama3.1-405b-stage16-ctx4096": 100}
 # the configurations timed beside the headline in the default run
 EXTRA_WORKLOADS = ("tinyllama-ctx256", "llama3-8b-batch64-ragged", "llama3-70b-stage20-batch16",
                    "llama3.1-8b-ctx131072")
@@ -533,6 +537,11 @@ def cpu_baseline(w: Workload, budget_s: float, cpu_layers: int):
     dim, kvd = nh * hd, nkv * hd
     variant = "v4" if cpu["avx512f"] else "v3"
     env_base = dict(os.environ, OMP_PROC_BIND="close", OMP_PLACES="cores", LEAP_REF_VARIANT=variant)
+    if dim > 8192:
+        # the reference's run_layer at this width holds 2 GiB of weights per
+        # layer, and the timed engine cycles several such layers
+        raise RuntimeError(f"no CPU leg at dim {dim}: the reference engine would hold "
+                           f"{4 * (2 * dim * dim + 2 * kvd * dim) / 2**30:.1f} GiB of weights per layer")
     ref_ok = (O.ref_q8_available() if w.is_q8 else O.ref_available()) and w.theta == 500000.0
     if ref_ok:
         kind = "block_q8" if w.is_q8 else "block" if w.is_block else "attention"
