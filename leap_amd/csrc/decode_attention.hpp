@@ -253,6 +253,22 @@ __device__ __forceinline__ float slice_sum(float x)
     return x + from_even_row(x);
 }
 
+// Max / sum over R rows of 16 lanes (R = 1, 2 or 4): rows 2k and 2k + 1
+// meet, then the two halves of the wave, through the lane crossbar
+// (ds_bpermute: no LDS storage, no barrier).  Every lane ends with the
+// result of its rows, the same bits in each (a + b == b + a).  The
+// permlane swaps would be cheaper, but given one value as both operands the
+// compiler takes their two results for one and folds max(p0, p1) to p0 and
+// p0 + p1 to p0 + p0.
+template <int R, bool MAX>
+__device__ __forceinline__ float rows_reduce(float x)
+{
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    if constexpr (R >= 2) x = op(x, __shfl_xor(x, 16));
+    if constexpr (R >= 4) x = op(x, __shfl_xor(x, 32));
+    return x;
+}
+
 // Max / sum over the score lanes (rows 1 and 3) of a value that is uniform
 // across the eight slice lanes of each K row; wave-uniform result.
 __device__ __forceinline__ float score_rows_max(float x)
@@ -892,18 +908,30 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     // laid out over those heads, with MGH record lanes per head: record lane
     // fg takes records fg, fg + MGH, ... as one batch of loads (n <= MGH * BW
     // a compile-time count, n_rt <= n; records [n_rt, n) read past the range,
-    // 0, and count as empty), and the lanes meet in LDS.  The (max, sum)
-    // pairs, which the D4 lanes of a record lane all need, are loaded once
-    // per (head, record) across the workgroup, ahead of the partial outputs,
-    // and shared through LDS: a load of each pair in every lane that needs it
-    // cost about 0.5 us at Llama-3-8B ctx 4096.
+    // 0, and count as empty).  With MGH <= 4 a wave holds MGH rows of 16
+    // lanes per 16 columns, one row per record lane, so that 16 adjacent
+    // lanes read 256 contiguous bytes of one record and the record lanes of
+    // a (head, column) meet across rows with lane swaps, without LDS or a
+    // barrier; with more record lanes (few heads) they meet in LDS.  (Record
+    // lanes in adjacent lanes, with one 16-byte column per record and lane,
+    // made the fold's loads four times slower to issue: 0.5-0.8 us at
+    // Llama-3-8B.)  The (max, sum) pairs, which the D4 lanes of a record
+    // lane all need, are loaded once per (head, record) across the
+    // workgroup, ahead of the partial outputs, and shared through LDS (at
+    // [head][record], so that the two halves of the heads use disjoint
+    // words): a load of each pair in every lane that needs it cost about
+    // 0.5 us at Llama-3-8B ctx 4096.
     auto fold_emit = [&](int h0, auto gh_c, int first, auto n_c, int n_rt) {
         constexpr int GH = decltype(gh_c)::value;
         constexpr int n = decltype(n_c)::value;
         constexpr int MGH = S::THREADS / (GH * D4);
-        static_assert(MGH * GH * D4 == S::THREADS, "fold layout");
+        static_assert(MGH * GH * D4 == S::THREADS && D4 % 16 == 0, "fold layout");
         static_assert(n <= MGH * BW && n <= kFinalMax, "records per lane");
-        const int fl = tid / (MGH * D4), fg = (tid / D4) % MGH, fd = tid % D4;  // head - h0, record lane, column
+        constexpr bool ROWS = MGH <= 4;
+        // head - h0, record lane, column
+        const int fl = tid / (MGH * D4);
+        const int fg = ROWS ? (tid / 16) % MGH : (tid / D4) % MGH;
+        const int fd = ROWS ? ((tid / (16 * MGH)) % (D4 / 16)) * 16 + tid % 16 : tid % D4;
         const int fh = h0 + fl;
         const bool flive = fh < G;
         constexpr int BL = (n + MGH - 1) / MGH;
@@ -929,14 +957,14 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 #pragma unroll
         for (int i = 0; i < MLT; i++) {
             const int t = tid + i * S::THREADS;
-            if (t < NML) ml_lds[t] = (t % n < n_rt) ? mlv[i] : make_float2(-INFINITY, 0.f);
+            if (t < NML) ml_lds[h0 * n + t] = (t % n < n_rt) ? mlv[i] : make_float2(-INFINITY, 0.f);
         }
         __syncthreads();
         float2 mlb[BL];
 #pragma unroll
         for (int j = 0; j < BL; j++) {
             const int c = fg + j * MGH;
-            mlb[j] = c < n ? ml_lds[fl * n + c] : make_float2(-INFINITY, 0.f);
+            mlb[j] = c < n ? ml_lds[fh * n + c] : make_float2(-INFINITY, 0.f);
         }
         float mm = -INFINITY, ll = 0.f;
         float4 oo = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -950,27 +978,38 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
             fma4(oo, w, ob[j]);
             ll += w * mlb[j].y;
         }
-        __syncthreads();  // LDS scratch is free
-        mo[(fl * MGH + fg) * D4 + fd] = oo;
-        if (fd == 0) {
-            mmx[fl * MGH + fg] = mm;
-            mls[fl * MGH + fg] = ll;
-        }
-        __syncthreads();
-        if (fg == 0 && flive) {
-            float Mx = -INFINITY;
-#pragma unroll
-            for (int g = 0; g < MGH; g++) Mx = fmaxf(Mx, mmx[fl * MGH + g]);
-            float Lx = 0.f;
-            float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int g = 0; g < MGH; g++) {
-                const float mgv = mmx[fl * MGH + g];
-                const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
-                fma4(ox, sc, mo[(fl * MGH + g) * D4 + fd]);
-                Lx += sc * mls[fl * MGH + g];
+        if constexpr (ROWS) {
+            // The record lanes meet across rows: max, rescale, sums.
+            const float Mx = rows_reduce<MGH, true>(mm);
+            const float sc = (mm == -INFINITY) ? 0.f : fast_exp2(mm - Mx);
+            const float4 ox =
+                make_float4(rows_reduce<MGH, false>(sc * oo.x), rows_reduce<MGH, false>(sc * oo.y),
+                            rows_reduce<MGH, false>(sc * oo.z), rows_reduce<MGH, false>(sc * oo.w));
+            const float Lx = rows_reduce<MGH, false>(sc * ll);
+            if (fg == 0 && flive) emit(fh, fd, ox, Mx, Lx);
+        } else {
+            __syncthreads();  // LDS scratch is free
+            mo[(fl * MGH + fg) * D4 + fd] = oo;
+            if (fd == 0) {
+                mmx[fl * MGH + fg] = mm;
+                mls[fl * MGH + fg] = ll;
             }
-            emit(fh, fd, ox, Mx, Lx);
+            __syncthreads();
+            if (fg == 0 && flive) {
+                float Mx = -INFINITY;
+#pragma unroll
+                for (int g = 0; g < MGH; g++) Mx = fmaxf(Mx, mmx[fl * MGH + g]);
+                float Lx = 0.f;
+                float4 ox = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int g = 0; g < MGH; g++) {
+                    const float mgv = mmx[fl * MGH + g];
+                    const float sc = (mgv == -INFINITY) ? 0.f : fast_exp2(mgv - Mx);
+                    fma4(ox, sc, mo[(fl * MGH + g) * D4 + fd]);
+                    Lx += sc * mls[fl * MGH + g];
+                }
+                emit(fh, fd, ox, Mx, Lx);
+            }
         }
     };
     // Fold records [first, first + n) of the G heads into (ox, Mx, Lx) of
