@@ -911,8 +911,9 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
     // 0, and count as empty).  With MGH <= 4 a wave holds MGH rows of 16
     // lanes per 16 columns, one row per record lane, so that 16 adjacent
     // lanes read 256 contiguous bytes of one record and the record lanes of
-    // a (head, column) meet across rows with lane swaps, without LDS or a
-    // barrier; with more record lanes (few heads) they meet in LDS.  (Record
+    // a (head, column) meet across rows through the lane crossbar
+    // (rows_reduce), without LDS or a barrier; with more record lanes (few
+    // heads) they meet in LDS.  (Record
     // lanes in adjacent lanes, with one 16-byte column per record and lane,
     // made the fold's loads four times slower to issue: 0.5-0.8 us at
     // Llama-3-8B.)  The (max, sum) pairs, which the D4 lanes of a record
