@@ -285,11 +285,17 @@ long long launch_cus(const LaunchShape &s, int n_seq, long long total_rows)
 // spreads its groups over the XCDs, when one per CU gives chunks of two
 // passes or more.  There one per CU measured 3.4-3.8 us faster than
 // one-pass chunks two per CU (one, two and four KV heads at ctx 32768, 16384
-// and 8192) and was no slower at the other sizes measured.
+// and 8192) and was no slower at the other sizes measured.  A launch with
+// sixteen q heads per KV head runs each cache head as two launch groups on
+// one XCD, which already doubles its workgroups: where the launch groups
+// cover every XCD, one per CU (chunks twice as long) measured 1.0-2.1 us
+// faster at the Llama-3.1-405B stage's 128/8/128, ctx 2048-8192 (ctx 4096
+// 17.9-18.5 -> 16.0-16.4 us).  With fewer launch groups than XCDs (two KV
+// heads at head_dim 64, ctx 4096) it was 0.5-0.7 us slower.
 int latency_per_cu(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
-    if (!spreads(s, n_seq, total_rows)) return 2;
+    if (!spreads(s, n_seq, total_rows)) return (s.kv_split && n_groups >= leap::kXcds) ? 1 : 2;
     const long long per_seq = std::max<long long>(1, (s.n_cu + n_groups / 2) / n_groups);
     const int pass = leap::rows_per_pass(s.head_dim, s.group, kWaves);
     return (max_T + per_seq - 1) / per_seq >= 2 * pass ? 1 : 2;
