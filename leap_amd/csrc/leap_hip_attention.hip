@@ -281,21 +281,30 @@ long long launch_cus(const LaunchShape &s, int n_seq, long long total_rows)
     return std::max<long long>(1, s.n_cu * n_groups / leap::kXcds);
 }
 
-// Workgroups per CU in the latency regime: two, except in a launch that
-// spreads its groups over the XCDs, when one per CU gives chunks of two
-// passes or more.  There one per CU measured 3.4-3.8 us faster than
-// one-pass chunks two per CU (one, two and four KV heads at ctx 32768, 16384
-// and 8192) and was no slower at the other sizes measured.  A launch with
-// sixteen q heads per KV head runs each cache head as two launch groups on
-// one XCD, which already doubles its workgroups: where the launch groups
-// cover every XCD, one per CU (chunks twice as long) measured 1.0-2.1 us
-// faster at the Llama-3.1-405B stage's 128/8/128, ctx 2048-8192 (ctx 4096
-// 17.9-18.5 -> 16.0-16.4 us).  With fewer launch groups than XCDs (two KV
-// heads at head_dim 64, ctx 4096) it was 0.5-0.7 us slower.
+// Workgroups per CU in the latency regime: two, except
+//   - in a launch of equal lengths with at least two (sequence, KV head)
+//     groups per XCD (counting the two launch groups of a cache head with
+//     sixteen q heads per KV head), which takes one per CU, with chunks twice
+//     as long.  Forced chunk lengths put the best there every time, and the
+//     rule measured 1.0-2.1 us faster at the Llama-3.1-405B stage's
+//     128/8/128 at ctx 2048-8192 (ctx 4096 17.7 -> 16.0 us), 0.75-0.97 us at
+//     32 KV heads of one q head (ctx 2048-4096), and 0.24-1.39 us for
+//     batches of 2-4 Llama-3-8B, 64/8/128 and TinyLlama sequences at ctx
+//     2048-4096.  With fewer groups (batch 1 at 8 KV heads; two KV heads at
+//     head_dim 64 with sixteen q heads each, 0.5-0.7 us slower) two per CU
+//     stays faster;
+//   - in a launch that spreads its groups over the XCDs, when one per CU
+//     gives chunks of two passes or more.  There one per CU measured 3.4-3.8
+//     us faster than one-pass chunks two per CU (one, two and four KV heads
+//     at ctx 32768, 16384 and 8192) and was no slower at the other sizes
+//     measured.
 int latency_per_cu(const LaunchShape &s, int n_seq, long long total_rows, int max_T)
 {
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
-    if (!spreads(s, n_seq, total_rows)) return (s.kv_split && n_groups >= leap::kXcds) ? 1 : 2;
+    if (!spreads(s, n_seq, total_rows)) {
+        const bool ragged = total_rows * 4 < 3ll * n_seq * max_T;
+        return (n_groups >= 2 * leap::kXcds && !ragged) ? 1 : 2;
+    }
     const long long per_seq = std::max<long long>(1, (s.n_cu + n_groups / 2) / n_groups);
     const int pass = leap::rows_per_pass(s.head_dim, s.group, kWaves);
     return (max_T + per_seq - 1) / per_seq >= 2 * pass ? 1 : 2;
