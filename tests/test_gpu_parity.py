@@ -263,21 +263,29 @@ def test_batched_small_ragged_with_tiny_contexts(split):
             _step_and_check(att, 0, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
 
 
-@pytest.mark.parametrize("nh,nkv,hd,Ts", [
-    (32, 8, 128, [1500, 1100]),          # 16 groups: 32 near-equal chunks each, asymmetric merge
-    (32, 8, 128, [500] * 7 + [5]),       # 64 groups: 8 chunks each, the short sequence 5 chunks of 1 row
-    (32, 4, 64, [6000]),                 # 4 groups: 128 near-equal chunks, two-level merge
-    (8, 1, 128, [20000]),                # one group: 512 near-equal chunks spread over the XCDs
-    (32, 8, 128, [6000, 5500]),          # 16 groups: 32 near-equal chunks of three passes
+@pytest.mark.parametrize("nh,nkv,hd,Ts,split", [
+    # at least two groups per XCD take one workgroup per CU:
+    (32, 8, 128, [1500, 1100], 0),       # 16 groups: 16 near-equal chunks each
+    (32, 8, 128, [500] * 7 + [5], 0),    # 64 groups: 4 chunks each, the short sequence 4 of 1-2 rows
+    (32, 8, 128, [6000, 5500], 0),       # 16 groups: 16 near-equal chunks of about six passes
+    (32, 8, 128, [2048] * 4, 0),         # 32 groups: 8 whole chunks of four passes each
+    (32, 32, 128, [2048], 0),            # 32 KV heads of one q head: the same
+    # fewer groups, two per CU:
+    (32, 4, 64, [6000], 0),              # 4 groups: 128 near-equal chunks, two-level merge
+    (8, 1, 128, [20000], 0),             # one group: 512 near-equal chunks spread over the XCDs
+    # forced: 32 one-pass chunks per sequence, 512 workgroups, the asymmetric merge of 32
+    (32, 8, 128, [4096, 4096], 128),
 ])
-def test_even_split_chunks(nh, nkv, hd, Ts):
-    """Launches that cut each sequence into a fixed number of near-equal
-    chunks (equal-length batches in the latency regime)."""
+def test_even_split_chunks(nh, nkv, hd, Ts, split):
+    """Equal-length batches in the latency regime: whole or near-equal
+    chunks, one or two workgroups per CU (and a forced chunk length)."""
     Ts = np.array(Ts)
     S = len(Ts)
     rng = rng_for(41, nh, nkv, hd, S)
     with HipAttention(nh, nkv, hd, int(Ts.max()) + 3, max_batch=S) as att:
         att.kv_fill_normal(0x4C454150 + 41, 1.0 / np.sqrt(hd))
+        if split:
+            att.set_split(split)
         q = normal(rng, (S, nh * hd), hd)
         k = normal(rng, (S, nkv * hd), hd)
         v = normal(rng, (S, nkv * hd), hd)
