@@ -3,14 +3,16 @@
     python -m leap_amd.build
 
 The RoPE table TU is compiled by the host C++ compiler with the reference's
-release flags, the checkpoint reader by the host compiler, and the HIP TU by
-hipcc for gfx950 only.  Packed-fp32 VALU
-instructions are disabled for device code (``-packed-fp32-ops``).
+release flags, the checkpoint reader by the host compiler, and the HIP TUs
+(the host side and the three kernel tables, see csrc/kernels.hpp) by hipcc
+for gfx950 only, in parallel.  Packed-fp32 VALU instructions are disabled for
+device code (``-packed-fp32-ops``).
 """
 from __future__ import annotations
 
 import os
 import shutil
+from concurrent.futures import ThreadPoolExecutor
 import subprocess
 import sys
 
@@ -46,24 +48,32 @@ def _run(cmd):
     return r
 
 
+HIP_SOURCES = ("leap_hip_attention", "kernels_decode", "kernels_decode_64", "kernels_decode_64p",
+               "kernels_decode_128", "kernels_decode_128p", "kernels_gemv", "kernels_q8")
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     rope_o = os.path.join(BUILD, "rope_table.o")
     ckpt_o = os.path.join(BUILD, "checkpoint.o")
-    hip_o = os.path.join(BUILD, "leap_hip_attention.o")
-    steps = [
+    hip_os = [os.path.join(BUILD, f"{n}.o") for n in HIP_SOURCES]
+    compile_steps = [
         ["g++", "-std=c++17", "-O3", "-march=x86-64-v3", "-ffast-math", "-fPIC", "-c",
          os.path.join(CSRC, "rope_table.cpp"), "-o", rope_o],
         ["g++", "-std=c++17", "-O2", "-Wall", "-fPIC", "-I", INCLUDE, "-c",
          os.path.join(CSRC, "checkpoint.cpp"), "-o", ckpt_o],
-        [_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
-         os.path.join(CSRC, "leap_hip_attention.hip"), "-o", hip_o],
-        [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", hip_o, rope_o, ckpt_o],
-    ]
-    for cmd in steps:
-        if verbose:
+    ] + [[_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, f"{n}.hip"), "-o", o]
+         for n, o in zip(HIP_SOURCES, hip_os)]
+    if verbose:
+        for cmd in compile_steps:
             print(" ".join(cmd))
-        _run(cmd)
+    jobs = max(1, min(len(compile_steps), os.cpu_count() or 1, 16))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, compile_steps))
+    link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", *hip_os, rope_o, ckpt_o]
+    if verbose:
+        print(" ".join(link))
+    _run(link)
     os.replace(LIB + ".tmp", LIB)
     # the C++20 engine-side wrapper and demo layer loop, linked against the
     # library in place

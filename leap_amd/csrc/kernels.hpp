@@ -1,0 +1,63 @@
+// The library's kernel tables, each instantiated in a translation unit of its
+// own so that the build compiles them in parallel:
+//   - kernels_decode.hip: the measurement kernels with the decode kernel's
+//     grids and the cross-XCD merge; kernels_decode_{64,64p,128,128p}.hip:
+//     the decode-attention kernels by head_dim and instance kind;
+//   - kernels_gemv.hip: the fp32 projection GEMVs by model width;
+//   - kernels_q8.hip: the int8 W8A8 projection GEMVs by width, group size,
+//     rows per team and input kind.
+// leap_hip_attention.hip holds the host side and picks kernels through these
+// functions only.
+#pragma once
+
+#include "decode_attention.hpp"
+#include "gemv.hpp"
+#include "gemv_q8.hpp"
+
+namespace leap_kernels {
+
+// Waves per workgroup of the decode kernel.
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * leap::kWave;
+
+// What a launch runs: the decode kernel, or one of the floor kernels with its
+// grid (measurement only).
+enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
+
+using KernelFn = void (*)(leap::StepArgs);
+using MergeFn = void (*)(leap::StepArgs);
+
+// The decode kernel (or a floor kernel) for head_dim hd and g q heads per
+// launch group; nullptr for a shape without one.
+//   part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
+//         long (leap::part_launch);
+//   kvs:  two launch groups of g heads per cache head (kv_split; g = 8 only);
+//   valu: the score and weighted-V products as VALU FMAs (the A/B knob).
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs);
+// The decode kernel alone, by head_dim HD and instance kind PART (one
+// translation unit per pair).
+template <int HD, bool PART>
+KernelFn pick_decode(int g, bool valu, bool kvs);
+extern template KernelFn pick_decode<64, false>(int, bool, bool);
+extern template KernelFn pick_decode<64, true>(int, bool, bool);
+extern template KernelFn pick_decode<128, false>(int, bool, bool);
+extern template KernelFn pick_decode<128, true>(int, bool, bool);
+
+// The cross-XCD merge of a spread launch.
+MergeFn pick_merge(int hd, int g);
+
+// The fp32 projections by dim = 1024 * NC: *rb rows per workgroup.
+using QkvFn = void (*)(leap::QkvArgs);
+using ProjFn = void (*)(leap::ProjArgs);
+bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb);
+
+// The int8 projections.
+using Q8Fn = void (*)(leap::Q8Args);
+// True if (dim, gs) has int8 kernels.
+bool q8_supported(int dim, int gs);
+// The kernel of `kind` (leap::kQ8InRms or leap::kQ8InF32) for `rows` rows:
+// the smallest compiled rows-per-team count RPT with kQ8Teams * RPT * n_cu >=
+// rows, else the largest; *rpt receives it.
+Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt);
+
+}  // namespace leap_kernels

@@ -1,0 +1,36 @@
+// Decode-attention kernel table (see kernels.hpp): the floor kernels and the
+// cross-XCD merge here, the decode kernel's instances by head_dim and
+// instance kind in kernels_decode_*.hip (compiled in parallel).
+#include "kernels.hpp"
+
+namespace leap_kernels {
+
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs)
+{
+    if (kind == kDecode) {
+        if (hd == 64) return part ? pick_decode<64, true>(g, valu, kvs) : pick_decode<64, false>(g, valu, kvs);
+        if (hd == 128) return part ? pick_decode<128, true>(g, valu, kvs) : pick_decode<128, false>(g, valu, kvs);
+        return nullptr;
+    }
+    if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8)) return nullptr;
+#define LEAP_CASE(HD, G)                                                                   \
+    if (hd == HD && g == G)                                                                \
+        return kind == kFloorLaunch ? leap::floor_launch_kernel<HD, G, kWaves>             \
+             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves> : nullptr;
+    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+#undef LEAP_CASE
+    return nullptr;
+}
+
+MergeFn pick_merge(int hd, int g)
+{
+#define LEAP_CASE(HD, G) \
+    if (hd == HD && g == G) return leap::part_merge_kernel<HD, G>;
+    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
+#undef LEAP_CASE
+    return nullptr;
+}
+
+}  // namespace leap_kernels

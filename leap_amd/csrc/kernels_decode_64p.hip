@@ -1,0 +1,6 @@
+// Decode kernel instances: head_dim 64, PART = true (see kernels_decode_table.hpp).
+#include "kernels_decode_table.hpp"
+
+namespace leap_kernels {
+template KernelFn pick_decode<64, true>(int g, bool valu, bool kvs);
+}  // namespace leap_kernels

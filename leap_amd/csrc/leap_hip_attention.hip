@@ -26,9 +26,7 @@
 #include <unistd.h>
 
 #include "checkpoint.hpp"
-#include "decode_attention.hpp"
-#include "gemv.hpp"
-#include "gemv_q8.hpp"
+#include "kernels.hpp"
 
 extern "C" void leap_rope_table_host(int seq_len, int head_size, float theta, float *cos_tab,
                                      float *sin_tab);
@@ -81,6 +79,8 @@ struct leap_hip_attention {
     std::string err;
 };
 
+using namespace leap_kernels;
+
 namespace {
 
 // The message of the last failure of a call made without a handle (create,
@@ -127,45 +127,6 @@ hipError_t launch_k(void (*fn)(P...), dim3 grid, dim3 block, hipStream_t stream,
 {
     void *kargs[] = {static_cast<void *>(&args)...};
     return hipLaunchKernel(reinterpret_cast<const void *>(fn), grid, block, kargs, 0, stream);
-}
-
-using KernelFn = void (*)(leap::StepArgs);
-
-// Waves per workgroup of the decode kernel.
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * leap::kWave;
-
-// What a launch runs: the decode kernel, or one of the floor kernels with its
-// grid (measurement only).
-enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
-
-// part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
-// long (leap::part_launch).
-// kvs: two launch groups of g heads per cache head (kv_split; g = 8 only).
-KernelFn pick_kernel(int hd, int g, int kind = kDecode, bool valu = false, bool part = false, bool kvs = false)
-{
-#define LEAP_CASE(HD, G)                                                                                   \
-    if (hd == HD && g == G && !kvs)                                                                        \
-        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>                           \
-               : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves>                           \
-               : part ? (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, true>                  \
-                              : leap::decode_attention_kernel<HD, G, kWaves, true, true>)                  \
-                      : (valu ? leap::decode_attention_kernel<HD, G, kWaves, false, false>                 \
-                              : leap::decode_attention_kernel<HD, G, kWaves, true, false>);
-#define LEAP_CASE_KVS(HD)                                                                                  \
-    if (hd == HD && g == 8 && kvs)                                                                         \
-        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, 8, kWaves>                           \
-               : kind == kFloorStream ? leap::floor_stream_kernel<HD, 8, kWaves>                           \
-               : part ? (valu ? leap::decode_attention_kernel<HD, 8, kWaves, false, true, true>            \
-                              : leap::decode_attention_kernel<HD, 8, kWaves, true, true, true>)            \
-                      : (valu ? leap::decode_attention_kernel<HD, 8, kWaves, false, false, true>           \
-                              : leap::decode_attention_kernel<HD, 8, kWaves, true, false, true>);
-    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
-    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
-    LEAP_CASE_KVS(64) LEAP_CASE_KVS(128)
-#undef LEAP_CASE
-#undef LEAP_CASE_KVS
-    return nullptr;
 }
 
 // How launches see a head shape: 16 q heads per KV head run as two groups
@@ -391,19 +352,6 @@ int max_chunks_for(int seq_len, int head_dim, int group, int n_kv_heads, int n_c
     return std::max(1, std::min(cap, std::max(by_pass, std::max(even, by_rows))));
 }
 
-using MergeFn = void (*)(leap::StepArgs);
-
-MergeFn pick_merge(int hd, int g)
-{
-#define LEAP_CASE(HD, G) \
-    if (hd == HD && g == G) return leap::part_merge_kernel<HD, G>;
-    LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
-    LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
-#undef LEAP_CASE
-    return nullptr;
-}
-
-
 // Enqueue one decode-attention launch.  Returns 0, or a HIP error code
 // (hipErrorInvalidValue for a shape without a kernel or a launch too large).
 hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_seq, const int *pos_dev,
@@ -512,86 +460,6 @@ int alloc_all(leap_hip_attention *h, std::initializer_list<std::pair<void **, si
     size_t i = 0;
     for (const auto &b : bufs) *b.first = made[i++];
     return 0;
-}
-
-// Projection kernels by dim = 1024 * NC; RB rows per workgroup keep 128 KiB
-// of weights in flight per workgroup (64 KiB and 256 KiB measured slower at
-// Llama-3-8B).
-using QkvFn = void (*)(leap::QkvArgs);
-using ProjFn = void (*)(leap::ProjArgs);
-template <int NC>
-constexpr int proj_rows() { return 32 / NC; }
-
-bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb)
-{
-#define LEAP_PROJ(NC)                                                             \
-    if (dim == 1024 * NC) {                                                       \
-        *qkv = leap::qkv_kernel<proj_rows<NC>(), NC>;                             \
-        *proj = leap::proj_residual_kernel<proj_rows<NC>(), NC>;                  \
-        *rb = proj_rows<NC>();                                                    \
-        return true;                                                              \
-    }
-    LEAP_PROJ(2) LEAP_PROJ(3) LEAP_PROJ(4) LEAP_PROJ(5) LEAP_PROJ(8)
-#undef LEAP_PROJ
-    return false;
-}
-
-using Q8Fn = void (*)(leap::Q8Args);
-
-// The int8 projection kernels by (values per thread E, lanes per group
-// L = gs/E, rows per team RPT, input kind, threads per team that own values
-// ACT; n = ACT * E).  RPT is compiled in (every load of a thread is then
-// unconditional); a launch takes the smallest instantiated RPT that covers
-// its rows with one workgroup per CU.
-struct Q8Entry {
-    int e, l, rpt, kind, act;
-    Q8Fn fn;
-};
-
-#define LEAP_Q8_K(E, L, R, K, A) {E, L, R, K, A, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms, A>},
-#define LEAP_Q8_QKV(E, L, A) LEAP_Q8_K(E, L, 2, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 3, leap::kQ8InRms, A) \
-    LEAP_Q8_K(E, L, 4, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 6, leap::kQ8InRms, A)                      \
-    LEAP_Q8_K(E, L, 8, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 10, leap::kQ8InRms, A)
-#define LEAP_Q8_PROJ(E, L, A) LEAP_Q8_K(E, L, 2, leap::kQ8InF32, A) LEAP_Q8_K(E, L, 4, leap::kQ8InF32, A) \
-    LEAP_Q8_K(E, L, 8, leap::kQ8InF32, A)
-#define LEAP_Q8_ALL(E, L, A) LEAP_Q8_QKV(E, L, A) LEAP_Q8_PROJ(E, L, A)
-const Q8Entry kQ8Kernels[] = {
-    // dim 2048, 4096, 8192: every thread of a team owns E = dim/256 values
-    LEAP_Q8_ALL(8, 4, 256) LEAP_Q8_ALL(8, 8, 256) LEAP_Q8_ALL(8, 16, 256)
-    LEAP_Q8_ALL(16, 2, 256) LEAP_Q8_ALL(16, 4, 256) LEAP_Q8_ALL(16, 8, 256) LEAP_Q8_ALL(16, 16, 256)
-    LEAP_Q8_ALL(32, 2, 256) LEAP_Q8_ALL(32, 4, 256) LEAP_Q8_ALL(32, 8, 256)
-    // dim 3072 (Llama-3.2-3B): 192 threads of 16 values; dim 5120 (Llama-2-13B): 160 of 32
-    LEAP_Q8_ALL(16, 2, 192) LEAP_Q8_ALL(16, 4, 192) LEAP_Q8_ALL(16, 8, 192)
-    LEAP_Q8_ALL(32, 2, 160) LEAP_Q8_ALL(32, 4, 160)
-};
-#undef LEAP_Q8_ALL
-#undef LEAP_Q8_PROJ
-#undef LEAP_Q8_QKV
-#undef LEAP_Q8_K
-
-// True if (dim, gs) has int8 kernels.
-bool q8_supported(int dim, int gs)
-{
-    for (const Q8Entry &k : kQ8Kernels)
-        if (k.act * k.e == dim && k.l * k.e == gs) return true;
-    return false;
-}
-
-// The kernel of `kind` for `rows` rows: the smallest RPT with 4 * RPT * n_cu
-// >= rows, else the largest; *rpt receives it.
-Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
-{
-    const int need = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
-    const Q8Entry *best = nullptr;
-    for (const Q8Entry &k : kQ8Kernels) {
-        if (k.act * k.e != dim || k.l * k.e != gs || k.kind != kind) continue;
-        const bool covers = k.rpt >= need, best_covers = best && best->rpt >= need;
-        if (!best || (covers && (!best_covers || k.rpt < best->rpt)) || (!covers && !best_covers && k.rpt > best->rpt))
-            best = &k;
-    }
-    if (!best) return nullptr;
-    *rpt = best->rpt;
-    return best->fn;
 }
 
 int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x, float *x_res, hipStream_t stream)
