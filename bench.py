@@ -58,6 +58,11 @@ beside `value`, never as `value`.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload NAME] [--no-cpu]
                     [--no-extra] [--no-host-pointer] [--no-graph]
+    python bench.py --timeline [--workload NAME] [--split N] [--fold-helper M]
+
+`--timeline` runs the workload on the library's timeline build instead and
+prints where each launch's time goes: per-workgroup device-clock stamps at the
+kernel's phase boundaries (see timeline_report).
 """
 from __future__ import annotations
 
@@ -251,7 +256,7 @@ class Workload:
     """One configuration on the device: the handle, its filled cache, the
     step's inputs, and one_step() running the layer sweep on `stream`."""
 
-    def __init__(self, workload: str, split: int = 0, valu: bool = False):
+    def __init__(self, workload: str, split: int = 0, valu: bool = False, lib=None):
         import torch
         from leap_amd.attention import HipAttention
         self.name = workload
@@ -262,7 +267,7 @@ class Workload:
         self.is_q8 = workload in Q8_WORKLOADS
         dev = torch.device("cuda:0")
         self.att = att = HipAttention(nh, nkv, hd, int(self.Ts.max()), n_layers=L, rope_theta=theta,
-                                      max_batch=batch)
+                                      max_batch=batch, lib=lib)
         if split:
             att.set_split(split)
         if valu:
@@ -434,6 +439,97 @@ def t_sweep():
     res["note"] = ("eager: one Python ctypes call per launch, which costs about 7 us of host time, so short "
                    "contexts are host-bound there; graph: the same launches replayed from a HIP graph")
     return res
+
+
+# ---- timeline (the library's timeline build) ---------------------------------------
+
+TL_POINTS = ("start", "prologue", "scored", "loop_end", "combined", "stored", "drained", "counted",
+             "fold_issued", "fold_loaded", "folded", "sub_counted", "sub_folded", "end")
+TL_ROLE, TL_HW, TL_WORDS, TL_SLOTS, TL_WGS = 14, 15, 16, 64, 2048
+TL_SINGLE, TL_FINAL, TL_HELPER, TL_SUB = 1, 2, 4, 8
+
+
+def timeline_report(workload: str, steps: int, warmup: int, split: int = 0, fold_helper: int = 1):
+    """Per-workgroup device-clock stamps of the workload's decode launches,
+    from the timeline build of the library (libleap_hip_attention_tl.so,
+    the same sources with LEAP_TIMELINE; see leap_hip_attention_timeline).
+    Over the last launches the ring holds (up to 64), each launch's stamps
+    are taken relative to its first workgroup's entry, in microseconds; the
+    report gives, per point, the median over launches of the median and of
+    the last workgroup to pass it, the final folder's and the fold helper's
+    own points, the launch end (the last workgroup's exit) and the gap to the
+    next launch's first workgroup."""
+    import ctypes
+    import torch
+    from leap_amd import attention as A
+    lib = A.load_timeline_library()
+    w = Workload(workload, split=split, lib=lib)
+    if fold_helper != 1:
+        w.att.set_fold_helper(fold_helper)
+    try:
+        for _ in range(warmup):
+            w.one_step()
+        n_steps = max(steps, -(-TL_SLOTS // w.L))
+        for _ in range(n_steps):
+            w.one_step()
+        torch.cuda.synchronize()
+        ring = np.zeros(TL_SLOTS * TL_WGS * TL_WORDS, np.uint64)
+        launches = ctypes.c_longlong(0)
+        rc = lib.leap_hip_attention_timeline(ring.ctypes.data, ring.nbytes, ctypes.byref(launches))
+        if rc != 0:
+            raise RuntimeError(f"leap_hip_attention_timeline returned {rc}")
+    finally:
+        w.close()
+    ring = ring.reshape(TL_SLOTS, TL_WGS, TL_WORDS)
+    n = min(TL_SLOTS, launches.value, n_steps * w.L)
+    order = [(launches.value - n + i) % TL_SLOTS for i in range(n)]
+    per = []
+    for j, slot in enumerate(order):
+        t = ring[slot].astype(np.int64)
+        st = t[:, 0]
+        live = st > 0
+        anchor = np.median(st[live])
+        wg = live & (np.abs(st - anchor) < 10_000)  # this launch's workgroups (100 us window)
+        t0 = st[wg].min()
+        rel = np.where(t[wg, :14] > 0, (t[wg, :14] - t0) / 100.0, np.nan)  # ticks of 10 ns -> us
+        role = t[wg, TL_ROLE]
+        r = {"n_wg": int(wg.sum()), "end": float(np.nanmax(rel[:, 13]))}
+        for k, name in enumerate(TL_POINTS[1:13], start=1):
+            col = rel[:, k]
+            if np.isfinite(col).any():
+                r[name] = (float(np.nanmedian(col)), float(np.nanmax(col)))
+        for tag, bit in (("final", TL_FINAL), ("helper", TL_HELPER)):
+            sel = (role & bit) != 0
+            if sel.any():
+                sub = rel[sel]
+                r[tag] = {name: float(np.nanmedian(sub[:, k])) for k, name in enumerate(TL_POINTS)
+                          if k > 0 and np.isfinite(sub[:, k]).any()}
+        if j + 1 < n:
+            nxt = ring[order[j + 1]].astype(np.int64)[:, 0]
+            nl = nxt > 0
+            nwin = nl & (np.abs(nxt - np.median(nxt[nl])) < 10_000)
+            r["gap_to_next"] = (nxt[nwin].min() - t0) / 100.0 - r["end"]
+        per.append(r)
+
+    def med(vals):
+        vals = [v for v in vals if v is not None]
+        return round(float(np.median(vals)), 3) if vals else None
+    out = {"workload": workload, "launches": n, "n_wg": int(np.median([r["n_wg"] for r in per])),
+           "launch_end_us": med([r["end"] for r in per]),
+           "gap_to_next_us": med([r.get("gap_to_next") for r in per]), "points_us": {}}
+    for name in TL_POINTS[1:13]:
+        have = [r[name] for r in per if name in r]
+        if have:
+            out["points_us"][name] = {"median_wg": med([h[0] for h in have]), "last_wg": med([h[1] for h in have])}
+    for tag in ("final", "helper"):
+        have = [r[tag] for r in per if tag in r]
+        if have:
+            out[tag + "_us"] = {name: med([h.get(name) for h in have]) for name in TL_POINTS[1:]
+                                if any(name in h for h in have)}
+    out["note"] = ("device clock (s_memrealtime, 100 MHz) per workgroup from libleap_hip_attention_tl.so, "
+                   "relative to each launch's first workgroup entry; medians over the launches; the stamps "
+                   "themselves cost a little (wave 0 keeps them in registers and stores them at exit)")
+    return out
 
 
 # ---- CPU baseline (the reference's own code, or the oracle) ------------------------
@@ -688,10 +784,19 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only run the workload on the library's timeline build and print the per-phase "
+                         "device-clock medians of its launches")
+    ap.add_argument("--fold-helper", type=int, default=1, choices=(0, 1, 2),
+                    help="the fold-helper mode of the timeline run (leap_hip_attention_set_fold_helper)")
     ap.add_argument("--cpu-leg", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_leg:
         cpu_leg_child(args.cpu_leg)
+        return
+    if args.timeline:
+        print(json.dumps(timeline_report(args.workload, args.steps or 8, args.warmup, args.split,
+                                         args.fold_helper)), flush=True)
         return
     if args.copy_probe:
         import torch

@@ -112,8 +112,10 @@ int leap_hip_attention_step_batched(leap_hip_attention *h, int layer, int n_seq,
 
 /* As leap_hip_attention_step_batched with device pointers (pos included),
  * enqueued on `stream`.  max_pos is a host-side upper bound of pos[] used to
- * size the launch; sequences whose pos lies outside [0, max_pos] or beyond
- * seq_len are skipped and their outputs left unwritten.  total_rows is the
+ * size the launch; a sequence whose pos lies outside [0, max_pos] or at or
+ * beyond seq_len is skipped: its cache rows are neither read nor written,
+ * and its output row is filled with NaN so that a caller's bad position
+ * cannot pass for attention output.  total_rows is the
  * host's sum of pos[i] + 1 when it has one (it only steers the split of the
  * positions over workgroups), or 0 when it does not: the launch is then
  * sized as if the sequences were spread evenly up to max_pos.  q, k_new,
@@ -143,20 +145,24 @@ int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, in
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).  The split-K workspace is
  * a 4 MiB static device array, one per device (held until the process ends):
- * a fixed 144 KiB region of arrival counters (n_kv_heads <= 128) and 33 KiB
- * of part records, then n_heads x 72 partial records of (head_dim + 2)
- * floats (for at least 8 KV heads' worth of q heads), at most 64 split-K
- * chunks per call (up to 107 heads of 128 or 211 heads of 64; Llama-3-8B
- * uses 1.38 MB, Llama-3-70B 2.58 MB); larger shapes return -EINVAL.  Every
- * call on one device shares that array: launches leave the counters at
- * zero and the first call on a device clears the array on its stream, so
- * calls that overlap on one GPU, on any streams, race.
+ * a fixed 144 KiB region of arrival counters for at most 128 launch groups
+ * (128 KV heads, or 64 with 16 q heads per KV head, whose heads run as two
+ * groups each) and 33 KiB of part records, then n_heads x 72 partial
+ * records of (head_dim + 2) floats (for at least 8 KV heads' worth of q
+ * heads), at most 64 split-K chunks per call (up to 107 heads of 128 or 211
+ * heads of 64; Llama-3-8B uses 1.38 MB, Llama-3-70B 2.58 MB); larger shapes
+ * return -EINVAL.  Every call on one device shares that array: launches
+ * leave the counters at zero, and the array is zero from the start (the
+ * first call on a device that is not under stream capture also clears it
+ * on its stream, ahead of its launch), so calls that overlap on one GPU,
+ * on any streams, race.
  *   cfg      n_heads, n_kv_heads, head_dim, seq_len and device are read
- *   rope     [seq_len][head_dim/2] (cos, sin) pairs, fp32 (the reference's
- *            rope_cos / rope_sin, FloatTransformer.cpp:56-72, interleaved)
+ *   rope     [seq_len][head_dim/2] (cos, sin) pairs of fp32: row p holds
+ *            cos(p * f_i), sin(p * f_i) for f_i = theta^(-2i/head_dim),
+ *            i < head_dim/2, each pair adjacent
  *   k_cache, v_cache  this layer's cache rows of the sequence,
- *            [seq_len][kv_dim] (FloatTransformer.cpp:396-398); row pos is
- *            written (rotated k, v)
+ *            [seq_len][kv_dim] row-major, kv_dim = n_kv_heads * head_dim;
+ *            row pos is written (rotated k, v)
  *   q, k_new, v_new, out   as leap_hip_attention_step_async
  * Device pointers, all 16-byte aligned; enqueued on `stream`.  Failures
  * are reported by leap_hip_attention_last_error(NULL). */
@@ -352,7 +358,10 @@ int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention
  * bare-stream floor).  pos is device memory as in step_batched_async, or
  * NULL for every sequence at max_pos.  Neither kind writes memory or
  * changes the cache.  n_seq = 1, pos = NULL, max_pos = the position,
- * total_rows = position + 1 is the single-sequence step. */
+ * total_rows = position + 1 is the single-sequence step.  -EINVAL for a
+ * launch whose step spreads its (sequence, KV head) groups over the XCDs
+ * (fewer than 8 groups of at least 4 MiB of rows each): the floor kernels
+ * have no spread grid. */
 int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, int n_seq, const int *pos,
                                    int max_pos, long long total_rows, void *stream);
 
@@ -361,6 +370,23 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
  * decode kernel's merge needs xcc_out[i] == xcc_out[i % 8] for every i;
  * leap_hip_attention_create checks that and returns -ENOTSUP otherwise. */
 int leap_hip_attention_xcc_map(int device, int n_wg, int *xcc_out);
+
+/* Per-workgroup timeline of the decode launches (measurement only; no
+ * counterpart in the reference).  Only the timeline build of the library,
+ * libleap_hip_attention_tl.so (compiled with LEAP_TIMELINE), records it; this
+ * library returns -ENOTSUP.  There, every decode launch since the first
+ * create stores, for each of its first 2048 workgroups, 16 64-bit words: the
+ * 100 MHz device clock (s_memrealtime) at fixed points of the kernel (entry,
+ * prologue, first scores, main loop end, wave combine, record or output
+ * stored, record drained, arrival counted, fold loads issued, fold pairs
+ * shared, fold stored, sub-group counted, sub-group stored, exit; 0 where a
+ * workgroup did not pass), its role bits (1 output written alone, 2 final
+ * fold, 4 fold helper, 8 sub-group fold) with its arrival count << 8, and
+ * XCC_ID << 32 | HW_ID.  Launch i writes slot i % 64 of a ring of
+ * 64 x 2048 x 16 words.  Copies the ring to dst (at least 16 MiB) and the
+ * number of launches so far to *launches; the caller synchronises its
+ * streams first. */
+int leap_hip_attention_timeline(void *dst, size_t bytes, long long *launches);
 
 #ifdef __cplusplus
 }

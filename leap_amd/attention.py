@@ -18,6 +18,9 @@ import os
 import numpy as np
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libleap_hip_attention.so")
+# the timeline build (the same sources compiled with LEAP_TIMELINE): decode
+# launches record per-workgroup device-clock stamps (leap_hip_attention_timeline)
+LIB_TL_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libleap_hip_attention_tl.so")
 
 _F = ctypes.POINTER(ctypes.c_float)
 _I = ctypes.c_int
@@ -37,7 +40,7 @@ EXPORTS = (
     "leap_hip_attention_load_checkpoint", "leap_hip_attention_packet_header",
     "leap_hip_attention_packet_upload", "leap_hip_attention_packet_download",
     "leap_hip_attention_xcc_map", "leap_hip_attention_step_noalloc", "leap_hip_attention_floor_async",
-    "leap_hip_attention_set_products", "leap_hip_attention_set_fold_helper",
+    "leap_hip_attention_set_products", "leap_hip_attention_set_fold_helper", "leap_hip_attention_timeline",
 )
 
 PACKET_HEADER_BYTES = 8
@@ -73,13 +76,28 @@ class Config(ctypes.Structure):
 
 
 _lib = None
+_lib_tl = None
 
 
 def load_library(path: str = LIB_PATH):
     """Load the HIP library; fails loudly when it has not been built."""
     global _lib
-    if _lib is not None:
-        return _lib
+    if _lib is None:
+        _lib = _open(path)
+    return _lib
+
+
+def load_timeline_library():
+    """Load the timeline build of the library (its own copy of every entry
+    point, with leap_hip_attention_timeline recording); handles made with it
+    are passed `lib=` this library."""
+    global _lib_tl
+    if _lib_tl is None:
+        _lib_tl = _open(LIB_TL_PATH)
+    return _lib_tl
+
+
+def _open(path: str):
     if not os.path.isfile(path):
         raise RuntimeError(f"{path} is missing: build it with `python -m leap_amd.build`")
     L = ctypes.CDLL(path)
@@ -117,11 +135,11 @@ def load_library(path: str = LIB_PATH):
     L.leap_hip_attention_set_products.argtypes = [H, _I]
     L.leap_hip_attention_set_fold_helper.argtypes = [H, _I]
     L.leap_hip_attention_step_noalloc.argtypes = [ctypes.POINTER(Config), _I] + [_P] * 8
+    L.leap_hip_attention_timeline.argtypes = [_P, ctypes.c_size_t, ctypes.POINTER(ctypes.c_longlong)]
     for name in EXPORTS:
         fn = getattr(L, name)
         if name != "leap_hip_attention_last_error":
             fn.restype = _I
-    _lib = L
     return L
 
 
@@ -185,8 +203,8 @@ class HipAttention:
     """One handle of the MI355X attention library (see the C header)."""
 
     def __init__(self, n_heads, n_kv_heads, head_dim, seq_len, n_layers=1, layer_begin=0,
-                 layer_end=None, rope_theta=500000.0, max_batch=1, device=0):
-        self.lib = load_library()
+                 layer_end=None, rope_theta=500000.0, max_batch=1, device=0, lib=None):
+        self.lib = lib if lib is not None else load_library()
         self.cfg = Config(n_layers, layer_begin, n_layers if layer_end is None else layer_end,
                           n_heads, n_kv_heads, head_dim, seq_len, rope_theta, max_batch, device)
         self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim

@@ -1,6 +1,6 @@
 """Build recipe for libleap_hip_attention.so (gfx950), in-tree.
 
-    python -m leap_amd.build
+    python -m leap_amd.build [--no-timeline]
 
 The RoPE table TU is compiled by the host C++ compiler with the reference's
 release flags, the checkpoint reader by the host compiler, and the HIP TUs
@@ -22,6 +22,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libleap_hip_attention.so")
+LIB_TL = os.path.join(PKG, "libleap_hip_attention_tl.so")  # the timeline build (-DLEAP_TIMELINE)
 DEMO = os.path.join(PKG, "host", "engine_demo")
 ARCH = "gfx950"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
@@ -52,29 +53,45 @@ HIP_SOURCES = ("leap_hip_attention", "kernels_decode", "kernels_decode_64", "ker
                "kernels_decode_128", "kernels_decode_128p", "kernels_gemv", "kernels_q8")
 
 
-def build(verbose: bool = False) -> str:
+def _hip_objects(build_dir: str, defines=()):
+    """Compile steps of the HIP translation units into build_dir."""
+    os.makedirs(build_dir, exist_ok=True)
+    objs = [os.path.join(build_dir, f"{n}.o") for n in HIP_SOURCES]
+    steps = [[_hipcc(), *HIPCC_FLAGS, *defines, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, f"{n}.hip"),
+              "-o", o] for n, o in zip(HIP_SOURCES, objs)]
+    return objs, steps
+
+
+def build(verbose: bool = False, timeline: bool = True) -> str:
+    """Build the library (and, with timeline, its timeline build
+    libleap_hip_attention_tl.so, the same sources with -DLEAP_TIMELINE)."""
     os.makedirs(BUILD, exist_ok=True)
     rope_o = os.path.join(BUILD, "rope_table.o")
     ckpt_o = os.path.join(BUILD, "checkpoint.o")
-    hip_os = [os.path.join(BUILD, f"{n}.o") for n in HIP_SOURCES]
+    hip_os, hip_steps = _hip_objects(BUILD)
     compile_steps = [
         ["g++", "-std=c++17", "-O3", "-march=x86-64-v3", "-ffast-math", "-fPIC", "-c",
          os.path.join(CSRC, "rope_table.cpp"), "-o", rope_o],
         ["g++", "-std=c++17", "-O2", "-Wall", "-fPIC", "-I", INCLUDE, "-c",
          os.path.join(CSRC, "checkpoint.cpp"), "-o", ckpt_o],
-    ] + [[_hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, f"{n}.hip"), "-o", o]
-         for n, o in zip(HIP_SOURCES, hip_os)]
+    ] + hip_steps
+    libs = [(LIB, hip_os)]
+    if timeline:
+        tl_os, tl_steps = _hip_objects(os.path.join(BUILD, "tl"), ("-DLEAP_TIMELINE",))
+        compile_steps += tl_steps
+        libs.append((LIB_TL, tl_os))
     if verbose:
         for cmd in compile_steps:
             print(" ".join(cmd))
     jobs = max(1, min(len(compile_steps), os.cpu_count() or 1, 16))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, compile_steps))
-    link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", LIB + ".tmp", *hip_os, rope_o, ckpt_o]
-    if verbose:
-        print(" ".join(link))
-    _run(link)
-    os.replace(LIB + ".tmp", LIB)
+    for lib, objs in libs:
+        link = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", lib + ".tmp", *objs, rope_o, ckpt_o]
+        if verbose:
+            print(" ".join(link))
+        _run(link)
+        os.replace(lib + ".tmp", lib)
     # the C++20 engine-side wrapper and demo layer loop, linked against the
     # library in place
     demo = ["g++", "-std=c++20", "-O2", "-Wall", "-I", INCLUDE, "-I", os.path.join(PKG, "host"),
@@ -90,4 +107,4 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, timeline="--no-timeline" not in sys.argv[1:]))

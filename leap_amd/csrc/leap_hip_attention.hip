@@ -25,6 +25,7 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
+#include "aux_kernels.hpp"
 #include "checkpoint.hpp"
 #include "kernels.hpp"
 
@@ -352,6 +353,16 @@ int max_chunks_for(int seq_len, int head_dim, int group, int n_kv_heads, int n_c
     return std::max(1, std::min(cap, std::max(by_pass, std::max(even, by_rows))));
 }
 
+#ifdef LEAP_TIMELINE
+// The timeline build's ring of per-launch stamps ([kTlSlots][kTlMaxWgs]
+// [kTlPoints] words), allocated by the first create on the device, and the
+// number of decode launches enqueued so far (launch i uses slot i %
+// kTlSlots).
+unsigned long long *g_tl_ring = nullptr;
+long long g_tl_launches = 0;
+constexpr size_t kTlRingWords = (size_t)leap::kTlSlots * leap::kTlMaxWgs * leap::kTlPoints;
+#endif
+
 // Enqueue one decode-attention launch.  Returns 0, or a HIP error code
 // (hipErrorInvalidValue for a shape without a kernel or a launch too large).
 hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_seq, const int *pos_dev,
@@ -400,6 +411,11 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
 
     a.spread_log2 = spread_log2;
     a.kv_split = s.kv_split;
+#ifdef LEAP_TIMELINE
+    a.tl = (g_tl_ring && kind == kDecode)
+               ? g_tl_ring + (size_t)(g_tl_launches++ % leap::kTlSlots) * leap::kTlMaxWgs * leap::kTlPoints
+               : nullptr;
+#endif
     a.ws_po = b.ws_po;
     a.ws_pml = b.ws_pml;
 
@@ -538,6 +554,35 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_r
     return 0;
 }
 
+// The kernel tables are compiled in translation units of their own, each
+// with its own code object, which the runtime would load onto a device at the
+// first launch of one of its kernels, allocating device memory then.  Asking
+// for one kernel's attributes in each loads them all at once, at create and
+// at the allocation-free step's set-up, so that no later launch allocates.
+hipError_t load_kernel_tables()
+{
+    int rpt = 0;
+    const void *fns[] = {
+        reinterpret_cast<const void *>(pick_kernel(64, 4, kDecode, false, false, false)),
+        reinterpret_cast<const void *>(pick_kernel(64, 4, kDecode, false, true, false)),
+        reinterpret_cast<const void *>(pick_kernel(128, 4, kDecode, false, false, false)),
+        reinterpret_cast<const void *>(pick_kernel(128, 4, kDecode, false, true, false)),
+        reinterpret_cast<const void *>(pick_kernel(128, 4, kFloorLaunch, false, false, false)),
+        reinterpret_cast<const void *>(pick_q8(4096, 64, leap::kQ8InRms, 6144, 256, &rpt)),
+    };
+    QkvFn qkv = nullptr;
+    ProjFn proj = nullptr;
+    int rb = 0;
+    pick_proj(4096, &qkv, &proj, &rb);
+    for (const void *f : fns) {
+        hipFuncAttributes attr;
+        if (!f) return hipErrorInvalidValue;
+        if (hipError_t e = hipFuncGetAttributes(&attr, f); e != hipSuccess) return e;
+    }
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void *>(qkv));
+}
+
 // Run the XCC probe over n_wg workgroups of the decode kernel's block size
 // on `device` and copy the XCC id of each to xcc_host[n_wg].
 int xcc_map(leap_hip_attention *h, int device, int n_wg, int *xcc_host)
@@ -647,6 +692,7 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     // legacy default stream (stream 0); other caller streams must be
     // synchronised by the caller first.
     CREATE_TRY(hipStreamCreate(&h->stream));
+    CREATE_TRY(load_kernel_tables());
     if (int prc = check_placement(h, c.device, 2 * h->n_cu)) return fail(prc);
     const size_t cache_bytes = (size_t)c.max_batch * h->slab_floats * sizeof(float);
     CREATE_TRY(hipMalloc(&h->k_cache, cache_bytes));
@@ -689,6 +735,12 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     CREATE_TRY(hipMalloc(&h->out_dev, (size_t)c.max_batch * h->q_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->blk, (size_t)(3 * h->q_dim + 2 * h->kv_dim) * sizeof(float)));
     h->w_set.assign(h->n_local, 0);
+#ifdef LEAP_TIMELINE
+    if (!g_tl_ring) {
+        CREATE_TRY(hipMalloc(&g_tl_ring, kTlRingWords * sizeof(unsigned long long)));
+        CREATE_TRY(hipMemsetAsync(g_tl_ring, 0, kTlRingWords * sizeof(unsigned long long), h->stream));
+    }
+#endif
     CREATE_TRY(hipStreamSynchronize(h->stream));
 #undef CREATE_TRY
     *out = h;
@@ -817,8 +869,9 @@ int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int po
     const KvView kvv = kv_view(group, c.n_kv_heads);
     if (c.seq_len <= 0) return set_err(nullptr, -EINVAL, "seq_len %d", c.seq_len);
     if (kvv.n_kv_heads > kScratchMaxKvHeads)
-        return set_err(nullptr, -EINVAL, "%d kv groups: the static workspace holds counters for %d",
-                       kvv.n_kv_heads, kScratchMaxKvHeads);
+        return set_err(nullptr, -EINVAL,
+                       "%d launch groups (%d kv heads of %d q heads): the static workspace holds counters for %d",
+                       kvv.n_kv_heads, c.n_kv_heads, group, kScratchMaxKvHeads);
     const unsigned long long slab_bytes = ((unsigned long long)c.seq_len + leap::rows_per_pass(c.head_dim, 1, kWaves)) *
                                           (unsigned long long)c.n_kv_heads * c.head_dim * sizeof(float);
     if (slab_bytes >= (1ull << 32))
@@ -843,11 +896,17 @@ int leap_hip_attention_step_noalloc(const leap_hip_attention_config *cfg, int po
         void *p = nullptr;
         hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e == hipSuccess) e = hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, c.device);
-        if (e == hipSuccess) {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (e == hipSuccess) e = hipStreamIsCapturing((hipStream_t)stream, &cap);
+        if (e == hipSuccess && cap == hipStreamCaptureStatusNone) e = load_kernel_tables();
+        if (e == hipSuccess && cap == hipStreamCaptureStatusNone) {
             // The arrival counters must start at zero (every launch leaves
-            // them at zero, and no shape's records overlap them): the whole
-            // array is cleared once, on the first call's stream, ahead of
-            // its launch.
+            // them at zero, and no shape's records overlap them).  The array
+            // is zero when the code object loads (it has no initialiser);
+            // it is also cleared once, on the first call's stream, ahead of
+            // its launch, unless that call is being captured: a clear
+            // recorded into the caller's graph would run again at every
+            // replay, under the feet of calls on other streams.
             e = launch_k(zero_ints_kernel, dim3(256), dim3(256), (hipStream_t)stream, static_cast<int *>(p),
                          kScratchBytes / sizeof(int));
         }
@@ -1277,6 +1336,11 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
     if (total_rows <= 0 || total_rows > (long long)n_seq * (max_pos + 1))
         return set_err(h, -EINVAL, "total_rows %lld outside [1, %lld]", total_rows, (long long)n_seq * (max_pos + 1));
     if (reinterpret_cast<uintptr_t>(pos) % 4) return set_err(h, -EINVAL, "pos must be 4-byte aligned");
+    if (spreads(shape_of(h), n_seq, total_rows))
+        return set_err(h, -EINVAL,
+                       "%d sequences of %d KV heads and %lld rows spread over the XCDs in the step; the floor "
+                       "kernels have no spread grid",
+                       n_seq, h->cfg.n_kv_heads, total_rows);
     HIP_TRY(h, hipSetDevice(h->cfg.device));
     // with pos NULL, every sequence at max_pos
     return launch(h, layer, n_seq, pos, max_pos, max_pos, total_rows, nullptr, nullptr, nullptr, h->out_dev,
@@ -1351,6 +1415,28 @@ int leap_hip_attention_load_checkpoint(leap_hip_attention *h, const char *path)
     }
     munmap(map, (size_t)c.file_bytes);
     return rc;
+}
+
+int leap_hip_attention_timeline(void *dst, size_t bytes, long long *launches)
+{
+#ifdef LEAP_TIMELINE
+    if (!dst || !launches) return set_err(nullptr, -EINVAL, "NULL buffer");
+    if (bytes < kTlRingWords * sizeof(unsigned long long))
+        return set_err(nullptr, -EINVAL, "the timeline ring is %zu bytes", kTlRingWords * sizeof(unsigned long long));
+    if (!g_tl_ring) return set_err(nullptr, -EINVAL, "no handle has been created");
+    const hipError_t e = hipMemcpy(dst, g_tl_ring, kTlRingWords * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(nullptr, -EIO, "timeline copy: %s", hipGetErrorString(e));
+    }
+    *launches = g_tl_launches;
+    return 0;
+#else
+    (void)dst;
+    (void)bytes;
+    (void)launches;
+    return set_err(nullptr, -ENOTSUP, "this library has no timeline: load libleap_hip_attention_tl.so");
+#endif
 }
 
 int leap_hip_attention_kv_device_ptr(leap_hip_attention *h, int seq, int layer, float **k,

@@ -28,6 +28,22 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(A.EXPORTS)
 
 
+def test_timeline_build_exports_the_same_symbols():
+    tl = A.load_timeline_library()
+    missing = [n for n in _declared() if not hasattr(tl, n)]
+    assert not missing, missing
+
+
+def test_timeline_is_refused_by_the_production_library():
+    lib = A.load_library()
+    buf = (ctypes.c_ulonglong * 16)()
+    n = ctypes.c_longlong(-1)
+    rc = lib.leap_hip_attention_timeline(ctypes.addressof(buf), ctypes.sizeof(buf), ctypes.byref(n))
+    assert rc == -errno.ENOTSUP
+    assert "timeline" in lib.leap_hip_attention_last_error(None).decode()
+    assert n.value == -1
+
+
 def _create(**kw):
     lib = A.load_library()
     base = dict(n_layers=2, layer_begin=0, layer_end=2, n_heads=8, n_kv_heads=2, head_dim=128,

@@ -539,3 +539,52 @@ def test_fold_helper_modes_agree(nh, nkv, hd, T):
             att.set_fold_helper(3)
     for i, o in enumerate(outs[1:], 1):
         assert np.array_equal(o, outs[0]), f"step {i} differs from the first"
+
+
+# ---- device positions the launch cannot serve --------------------------------------
+
+@pytest.mark.parametrize("nh,nkv,hd,sl,Ts,bad", [
+    (32, 8, 128, 3000, (2500, 1200, 2900, 700), (1, -1)),     # a negative position
+    (32, 8, 128, 3000, (2500, 1200, 2900, 700), (2, 3000)),   # at seq_len
+    (32, 8, 128, 3000, (2500, 1200, 2900, 700), (0, 2950)),   # past the launch's max_pos
+    (32, 4, 64, 600, (400, 599, 64, 200), (3, -7)),           # TinyLlama heads, one chunk for some
+    (128, 8, 128, 1000, (999, 300, 512, 64), (2, 1000)),      # sixteen q heads per KV head (two groups each)
+    (16, 2, 128, 9100, (9000, 8800), (1, 9100)),              # few KV heads: spread over the XCDs
+])
+def test_batched_async_bad_position_writes_nan_rows(nh, nkv, hd, sl, Ts, bad):
+    """step_batched_async with one sequence at a position the launch cannot
+    serve (negative, at seq_len, or past max_pos): that sequence's output
+    row is all NaN and its cache untouched; every other sequence matches the
+    oracle as usual."""
+    import torch
+    n = len(Ts)
+    bad_seq, bad_pos = bad
+    rng = rng_for(77, nh, nkv, n, bad_seq, abs(bad_pos))
+    theta = 500000.0
+    with HipAttention(nh, nkv, hd, sl, max_batch=n) as att:
+        rows = []
+        for s, T in enumerate(Ts):
+            kr, vr = normal(rng, (T - 1, nkv * hd), hd), normal(rng, (T - 1, nkv * hd), hd)
+            att.kv_upload(s, 0, 0, kr, vr)
+            rows.append((kr, vr))
+        before = att.kv_download(bad_seq, 0, 0, sl)
+        pos = np.array([T - 1 for T in Ts], np.int32)
+        max_pos = int(pos.max())
+        pos[bad_seq] = bad_pos
+        q, k, v = normal(rng, (n, nh * hd), hd), normal(rng, (n, nkv * hd), hd), normal(rng, (n, nkv * hd), hd)
+        dq, dk, dv = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        out = torch.zeros(n, nh * hd, device="cuda:0")
+        dpos = torch.from_numpy(pos).cuda()
+        s = torch.cuda.Stream()
+        att.step_batched_async(0, n, dpos.data_ptr(), max_pos, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                               out.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        got = out.cpu().numpy()
+        assert np.isnan(got[bad_seq]).all(), "the skipped sequence's row is not all NaN"
+        after = att.kv_download(bad_seq, 0, 0, sl)
+        assert np.array_equal(before[0], after[0]) and np.array_equal(before[1], after[1])
+        for i, T in enumerate(Ts):
+            if i == bad_seq:
+                continue
+            assert np.isfinite(got[i]).all()
+            _step_and_check(att, 0, T - 1, q[i], k[i], v[i], theta, seq=i, out=got[i])

@@ -39,21 +39,25 @@ def test_xcc_map_is_periodic_in_eight(n_wg):
 
 
 def test_oversize_create_returns_enomem_and_frees_everything():
+    """create fails with -ENOMEM and frees what it had allocated: when its
+    first allocation (the key cache) already exceeds free memory, so that
+    nothing is held, and when the key cache fits and the value cache of the
+    same size does not (the key cache sized at just over half of free
+    memory, held only until the value cache's allocation fails)."""
     import torch
     torch.cuda.synchronize()
     free0, total = torch.cuda.mem_get_info()
-    # each cache slab of 32 layers x 131072 positions x 1024 floats is 16 GiB;
-    # size the key cache at ~60% of free memory, so that it succeeds and the
-    # value cache of the same size does not
-    per_seq = 32 * 131072 * 1024 * 4
-    max_batch = int(0.6 * free0 // per_seq) + 1
-    assert 2 * max_batch * per_seq > free0
-    with pytest.raises(LeapError) as ei:
-        HipAttention(32, 8, 128, 131072, n_layers=32, max_batch=max_batch)
-    assert ei.value.code == -errno.ENOMEM, str(ei.value)
-    torch.cuda.synchronize()
-    free1, _ = torch.cuda.mem_get_info()
-    assert abs(free1 - free0) <= 64 << 20, f"free memory {free0} before, {free1} after the failed create"
+    per_seq = 32 * 131072 * 1024 * 4  # one 16 GiB slab per cache
+    for frac, what in ((1.0, "first allocation"), (0.52, "second allocation")):
+        max_batch = int(frac * free0 // per_seq) + 1
+        assert max_batch * per_seq <= free0 or frac == 1.0
+        assert 2 * max_batch * per_seq > free0
+        with pytest.raises(LeapError) as ei:
+            HipAttention(32, 8, 128, 131072, n_layers=32, max_batch=max_batch)
+        assert ei.value.code == -errno.ENOMEM, f"{what}: {ei.value}"
+        torch.cuda.synchronize()
+        free1, _ = torch.cuda.mem_get_info()
+        assert abs(free1 - free0) <= 64 << 20, f"{what}: free memory {free0} before, {free1} after the failed create"
     # a normal handle still works
     rng = rng_for(91)
     with HipAttention(8, 2, 128, 64) as att:
@@ -118,3 +122,12 @@ def test_floor_launches_write_nothing(kind):
             att.floor_async(kind, 1, 4, T - 1, T, s.cuda_stream)
         with pytest.raises(LeapError):  # positions not 4-byte aligned
             att.floor_async(kind, 1, 1, T - 1, T, s.cuda_stream, pos_ptr=pos.data_ptr() + 2)
+    # a step that spreads its groups over the XCDs (one KV head, 4 MiB of
+    # rows) has no floor grid: refused rather than measured on another grid
+    with HipAttention(8, 1, 128, 8192) as att:
+        s = torch.cuda.Stream()
+        att.floor_async(kind, 0, 1, 1999, 2000, s.cuda_stream)  # 2 MiB of rows: one XCD, no spread
+        with pytest.raises(LeapError) as ei:
+            att.floor_async(kind, 0, 1, 8191, 8192, s.cuda_stream)
+        assert "spread" in str(ei.value)
+        s.synchronize()

@@ -129,3 +129,65 @@ def test_noalloc_alternating_shapes_share_the_workspace():
     finally:
         for att in atts:
             att.close()
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from leap_amd import attention as A
+from leap_amd.attention import HipAttention
+
+nh, nkv, hd, sl, pos = 32, 8, 128, 4096, 4095   # 64 chunks: the asymmetric merge
+dev = torch.device("cuda:0")
+with HipAttention(nh, nkv, hd, sl) as att:
+    att.kv_fill_normal(0x4341, 1.0 / np.sqrt(hd))
+    c, s_ = att.rope_download()
+    rope = torch.from_numpy(np.stack([c, s_], axis=-1).reshape(-1).copy()).cuda()
+    k0, v0 = att.kv_download(0, 0, 0, sl)
+    kc, vc = torch.from_numpy(k0).cuda(), torch.from_numpy(v0).cuda()
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    q = torch.randn(nh * hd, device=dev, generator=g) / np.sqrt(hd)
+    k = torch.randn(nkv * hd, device=dev, generator=g) / np.sqrt(hd)
+    v = torch.randn(nkv * hd, device=dev, generator=g) / np.sqrt(hd)
+    out_n = torch.full((nh * hd,), float("nan"), device=dev)
+    out_h = torch.full((nh * hd,), float("nan"), device=dev)
+    st = torch.cuda.Stream()
+    att.step_async(0, pos, q.data_ptr(), k.data_ptr(), v.data_ptr(), out_h.data_ptr(), st.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):  # the process's first no-alloc call
+        A.step_noalloc(nh, nkv, hd, sl, pos, rope.data_ptr(), kc.data_ptr(), vc.data_ptr(), q.data_ptr(),
+                       k.data_ptr(), v.data_ptr(), out_n.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out_n.fill_(float("nan"))
+        x = torch.randn(1 << 20, device=dev)  # other eager work between the replays
+        assert np.isfinite((x * 2).sum().item())
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_n, out_h), f"replay {rep} differs from the handle's step"
+    # eager calls after the replays still agree (the counters were left at zero)
+    out_n.fill_(float("nan"))
+    A.step_noalloc(nh, nkv, hd, sl, pos, rope.data_ptr(), kc.data_ptr(), vc.data_ptr(), q.data_ptr(),
+                   k.data_ptr(), v.data_ptr(), out_n.data_ptr(), st.cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out_n, out_h), "eager call after the replays differs"
+print("FIRST_CALL_CAPTURED_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """In a fresh process, the first call on the device is captured into a
+    HIP graph (so the static workspace's one-time clear is not recorded
+    into it) and replayed four times, with other eager work between; every
+    replay and a later eager call equal the handle's step bitwise."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "FIRST_CALL_CAPTURED_OK" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
