@@ -19,13 +19,16 @@ The default run's line also carries, for the same build and box:
     K/V rows with the same loads; the per-launch cost any one-launch design
     pays at this shape;
   - `workloads`: the other configurations, each allocated, filled, timed
-    (events over >= 10 steps) and freed in turn: TinyLlama ctx 256, a batch
-    of 64 Llama-3-8B sequences with ragged contexts in [512, 8192], a
-    Llama-3-70B pipeline stage (20 layers, batch 16, ctx 8192) and
-    Llama-3.1-8B at ctx 131072;
+    (events over >= 10 steps) and freed in turn, each with its same-grid
+    stream floor: TinyLlama ctx 256, a batch of 64 Llama-3-8B sequences with
+    ragged contexts in [512, 8192], a Llama-3-70B pipeline stage (20 layers,
+    batch 16, ctx 8192), Llama-3.1-8B at ctx 131072, and the Llama-3-8B
+    attention sub-block at ctx 4096 with fp32 and with int8 weights;
   - `t_sweep`: microseconds per layer-step over contexts 1 .. 16384 at the
     Llama-3-8B and TinyLlama head shapes, eager and replayed from a HIP graph
-    (every decode walks these contexts from position 0);
+    (every decode walks these contexts from position 0), and a generation's
+    mean over T = 1 .. 4096 at Llama-3-8B from every 32nd context
+    (`mean_us_per_layer_step_T1_4096`);
   - `cpu_baseline`: the reference's own code (oracle/_ref, built from its
     sources with its release flags) on the host cores, in a child process
     pinned as the reference's README says (OMP_PROC_BIND=close,
@@ -122,7 +125,7 @@ DEFAULT_STEPS = {"llama3-8b-ctx4096": 100, "tinyllama-ctx256": 2000,
                  "llama3.1-405b-stage16-ctx4096": 100}
 # the configurations timed beside the headline in the default run
 EXTRA_WORKLOADS = ("tinyllama-ctx256", "llama3-8b-batch64-ragged", "llama3-70b-stage20-batch16",
-                   "llama3.1-8b-ctx131072")
+                   "llama3.1-8b-ctx131072", "llama3-8b-block-ctx4096", "llama3-8b-q8-block-ctx4096")
 SWEEP_T = (1, 16, 64, 256, 512, 1024, 2048, 2304, 3072, 4096, 6144, 8192, 16384)
 SWEEP_SHAPES = {"llama3-8b": (32, 32, 8, 128, 500000.0), "tinyllama": (22, 32, 4, 64, 10000.0)}
 
@@ -337,7 +340,9 @@ class Workload:
 
     def floor_us(self, kind: int, steps: int, warmup: int) -> float:
         """Microseconds per layer-step of the floor launches (kind 1: the
-        launch alone, kind 2: the bare K/V stream) with this step's shape."""
+        launch alone, kind 2: the bare K/V stream; kind 3, sub-block
+        workloads: both projections streaming their weights alone around the
+        bare K/V stream) with this step's shape."""
         att, sp, L = self.att, self.stream.cuda_stream, self.L
         n, mp, tr = self.batch, self.max_pos, (self.total_rows if self.batch > 1 else self.max_pos + 1)
         pp = self.pos_dev.data_ptr() if self.batch > 1 else None
@@ -383,7 +388,7 @@ def extra_workload(name: str):
     try:
         r = measure(w, steps, 3)
         ok = w.finite()
-        floor = w.floor_us(2, steps, 3) if not w.is_block else None
+        floor = w.floor_us(3 if w.is_block else 2, steps, 3)
     finally:
         w.close()
         torch.cuda.synchronize()
@@ -401,6 +406,9 @@ def extra_workload(name: str):
                                                              "sum": int(Ts.sum())}},
         "stream_floor_us_per_layer_step": round(floor, 3) if floor else None,
         "stream_floor_frac": round(r["bytes_per_launch"] / (floor * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if floor else None,
+        "stream_floor_note": ("three launches per layer-step: the q/k/v and wo projections' grids streaming their "
+                              "weights alone around the attention's bare K/V stream") if w.is_block else
+                             "the step's grid streaming its K/V rows alone",
         "finite": ok,
     }
 
@@ -436,9 +444,56 @@ def t_sweep():
             res[name] = {"n_layers": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "T": rows}
         finally:
             att.close()
-    res["note"] = ("eager: one Python ctypes call per launch, which costs about 7 us of host time, so short "
-                   "contexts are host-bound there; graph: the same launches replayed from a HIP graph")
+    res["note"] = ("eager: one Python ctypes call per launch (the launch floor of about 3-4 us per launch from "
+                   "Python), so the shortest contexts are host-bound there; graph: the same launches replayed "
+                   "from a HIP graph")
+    gen = generation_sweep()
+    res["generation_llama3-8b"] = gen
+    res["mean_us_per_layer_step_T1_4096"] = gen["mean_us_per_layer_step_T1_4096"]
+    res["mean_graph_us_per_layer_step_T1_4096"] = gen["mean_graph_us_per_layer_step_T1_4096"]
     return res
+
+
+GEN_T = (1, 2, 4, 8, 16) + tuple(range(32, 4097, 32))
+
+
+def generation_sweep(steps: int = 20):
+    """A generation's decode steps at the Llama-3-8B head shape (32 layers):
+    the reference's generate loop walks T = pos + 1 from 1 to the context
+    (main.cpp:77-82).  Microseconds per layer-step at every 32nd context
+    (and 1-16), eager and replayed from a HIP graph, and their mean over T =
+    1..4096 with the samples joined linearly (one value per T)."""
+    import torch
+    from leap_amd.attention import HipAttention
+    L, nh, nkv, hd, th = SWEEP_SHAPES["llama3-8b"]
+    dev = torch.device("cuda:0")
+    att = HipAttention(nh, nkv, hd, max(GEN_T), n_layers=L, rope_theta=th)
+    eager, graph = [], []
+    try:
+        att.kv_fill_normal(SEED + 12, 1 / np.sqrt(hd))
+        q = torch.randn(L, nh * hd, device=dev) / np.sqrt(hd)
+        k = torch.randn(L, nkv * hd, device=dev) / np.sqrt(hd)
+        v = torch.randn(L, nkv * hd, device=dev) / np.sqrt(hd)
+        out = torch.empty(L, nh * hd, device=dev)
+        s = torch.cuda.Stream()
+        sp = s.cuda_stream
+        ptrs = [(q[l].data_ptr(), k[l].data_ptr(), v[l].data_ptr(), out[l].data_ptr()) for l in range(L)]
+        for T in GEN_T:
+            def one_step():
+                for l in range(L):
+                    att.step_async(l, T - 1, *ptrs[l], sp)
+            ms, _, _ = timed_steps(one_step, s, steps, 3, L)
+            eager.append(ms * 1e3 / (steps * L))
+            graph.append(hip_graph_us(one_step, s, steps, L))
+    finally:
+        att.close()
+    allT = np.arange(1, 4097)
+    return {
+        "n_layers": L, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd,
+        "T": list(GEN_T), "eager_us": [round(x, 3) for x in eager], "graph_us": [round(x, 3) for x in graph],
+        "mean_us_per_layer_step_T1_4096": round(float(np.interp(allT, GEN_T, eager).mean()), 3),
+        "mean_graph_us_per_layer_step_T1_4096": round(float(np.interp(allT, GEN_T, graph).mean()), 3),
+    }
 
 
 # ---- timeline (the library's timeline build) ---------------------------------------

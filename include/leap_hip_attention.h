@@ -358,7 +358,12 @@ int leap_hip_attention_block_views_get(leap_hip_attention *h, leap_hip_attention
  * bare-stream floor).  pos is device memory as in step_batched_async, or
  * NULL for every sequence at max_pos.  Neither kind writes memory or
  * changes the cache.  n_seq = 1, pos = NULL, max_pos = the position,
- * total_rows = position + 1 is the single-sequence step.  -EINVAL for a
+ * total_rows = position + 1 is the single-sequence step.  Kind 3, for a
+ * layer with weights set (one sequence, pos NULL, total_rows = max_pos +
+ * 1): the floor of leap_hip_attention_block_async, three launches with the
+ * grids, block sizes and weight loads of its q/k/v and wo projections
+ * streaming their weights (and int8 scales) alone, around the kind 2 launch
+ * of its attention step.  -EINVAL for a
  * launch whose step spreads its (sequence, KV head) groups over the XCDs
  * (fewer than 8 groups of at least 4 MiB of rows each): the floor kernels
  * have no spread grid. */

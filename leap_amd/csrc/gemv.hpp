@@ -179,4 +179,21 @@ __global__ __launch_bounds__(kGemvThreads) void proj_residual_kernel(ProjArgs a)
     }
 }
 
+// The weights alone (measurement only): the grid, block size and row loads of
+// qkv_kernel / proj_residual_kernel over w [rows][n], summed and kept only
+// behind a test that real data never meets.  The launch plus the bare weight
+// stream of one projection.
+template <int RB, int NC>
+__global__ __launch_bounds__(kGemvThreads) void gemv_floor_kernel(const float *w, int rows, float *sink)
+{
+    gemv_f4 wv[RB][NC];
+    issue_rows<RB, NC>(w, rows, blockIdx.x * RB, NC * 4 * kGemvThreads, wv);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < RB; i++)
+#pragma unroll
+        for (int c = 0; c < NC; c++) s += (wv[i][c].x + wv[i][c].y) + (wv[i][c].z + wv[i][c].w);
+    if (__builtin_bit_cast(unsigned, s) == 0x7FC0DEADu) sink[threadIdx.x] = s;
+}
+
 }  // namespace leap

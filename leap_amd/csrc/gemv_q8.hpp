@@ -374,4 +374,49 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
     }
 }
 
+// The int8 weights alone (measurement only): the grid, block size, scale
+// loads and row loads of q8_gemv_kernel<E, L, RPT, ..., ACT> over w [rows][n]
+// and its scales ws [rows][n / gs], summed and kept only behind a test that
+// real data never meets.  The launch plus the bare weight stream of one
+// int8 projection.
+template <int E, int L, int RPT, int ACT = kGemvThreads>
+__global__ __launch_bounds__(kQ8Threads) void q8_floor_kernel(Q8Args a)
+{
+    constexpr int n = ACT * E;
+    constexpr int NG = ACT / L;
+    constexpr int SLOTS = kQ8Teams * RPT;
+    constexpr int SCL = (RPT * NG / 4 + kGemvThreads - 1) / kGemvThreads;
+    const int tid = threadIdx.x;
+    const int team = tid / kGemvThreads, tt = tid % kGemvThreads;
+    const int rbase = blockIdx.x * SLOTS + team * RPT;
+    gemv_f4 scv[SCL];
+#pragma unroll
+    for (int i = 0; i < SCL; i++) {
+        const int e = 4 * (tt + i * kGemvThreads);
+        const int r = min(rbase + e / NG, a.rows - 1);
+        scv[i] = e < RPT * NG ? __builtin_nontemporal_load(reinterpret_cast<const gemv_f4 *>(a.ws + (size_t)r * NG + e % NG))
+                              : gemv_f4{0.f, 0.f, 0.f, 0.f};
+    }
+    Q8Row<E> wv[RPT];
+    const uint32_t w_bytes = (uint32_t)a.rows * (uint32_t)n;
+    const __amdgpu_buffer_rsrc_t w_rsrc = make_rsrc(a.w, w_bytes);
+#pragma unroll
+    for (int j = 0; j < RPT; j++) {
+        const int r = min(rbase + j, a.rows - 1);
+        if constexpr (ACT == kGemvThreads)
+            wv[j] = load_row_nt<E>(a.w + (size_t)r * n + tt * E);
+        else
+            wv[j] = load_row_buf<E>(w_rsrc, tt < ACT ? (uint32_t)r * (uint32_t)n + (uint32_t)(tt * E) : w_bytes);
+    }
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < RPT; j++)
+#pragma unroll
+        for (int k = 0; k < E / 4; k++) acc ^= wv[j].v[k];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < SCL; i++) s += (scv[i].x + scv[i].y) + (scv[i].z + scv[i].w);
+    if (acc == 0x7EADBEEF && __builtin_bit_cast(unsigned, s) == 0x7FC0DEADu) a.out0[tid] = s;
+}
+
 }  // namespace leap

@@ -49,7 +49,9 @@ MergeFn pick_merge(int hd, int g);
 // The fp32 projections by dim = 1024 * NC: *rb rows per workgroup.
 using QkvFn = void (*)(leap::QkvArgs);
 using ProjFn = void (*)(leap::ProjArgs);
-bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb);
+// (w, rows, sink): the same grid streaming the weights alone (measurement)
+using GemvFloorFn = void (*)(const float *, int, float *);
+bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb, GemvFloorFn *floor = nullptr);
 
 // The int8 projections.
 using Q8Fn = void (*)(leap::Q8Args);
@@ -57,7 +59,8 @@ using Q8Fn = void (*)(leap::Q8Args);
 bool q8_supported(int dim, int gs);
 // The kernel of `kind` (leap::kQ8InRms or leap::kQ8InF32) for `rows` rows:
 // the smallest compiled rows-per-team count RPT with kQ8Teams * RPT * n_cu >=
-// rows, else the largest; *rpt receives it.
-Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt);
+// rows, else the largest; *rpt receives it, and *floor (if not null) the
+// kernel with the same grid that streams the weights alone (measurement).
+Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt, Q8Fn *floor = nullptr);
 
 }  // namespace leap_kernels

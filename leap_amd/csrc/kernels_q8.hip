@@ -11,9 +11,11 @@ namespace leap_kernels {
 struct Q8Entry {
     int e, l, rpt, kind, act;
     Q8Fn fn;
+    Q8Fn floor;  // the same grid streaming the weights alone (measurement)
 };
 
-#define LEAP_Q8_K(E, L, R, K, A) {E, L, R, K, A, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms, A>},
+#define LEAP_Q8_K(E, L, R, K, A) \
+    {E, L, R, K, A, leap::q8_gemv_kernel<E, L, R, K, K != leap::kQ8InRms, A>, leap::q8_floor_kernel<E, L, R, A>},
 #define LEAP_Q8_QKV(E, L, A) LEAP_Q8_K(E, L, 2, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 3, leap::kQ8InRms, A) \
     LEAP_Q8_K(E, L, 4, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 6, leap::kQ8InRms, A)                      \
     LEAP_Q8_K(E, L, 8, leap::kQ8InRms, A) LEAP_Q8_K(E, L, 10, leap::kQ8InRms, A)
@@ -44,7 +46,7 @@ bool q8_supported(int dim, int gs)
 
 // The kernel of `kind` for `rows` rows: the smallest RPT with 4 * RPT * n_cu
 // >= rows, else the largest; *rpt receives it.
-Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
+Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt, Q8Fn *floor)
 {
     const int need = (rows + leap::kQ8Teams * n_cu - 1) / (leap::kQ8Teams * n_cu);
     const Q8Entry *best = nullptr;
@@ -56,6 +58,7 @@ Q8Fn pick_q8(int dim, int gs, int kind, int rows, int n_cu, int *rpt)
     }
     if (!best) return nullptr;
     *rpt = best->rpt;
+    if (floor) *floor = best->floor;
     return best->fn;
 }
 

@@ -520,6 +520,55 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     return 0;
 }
 
+// The floor of the sub-block (measurement only; leap_hip_attention_floor_async
+// kind 3): the q/k/v projection's and the wo projection's grids streaming
+// their weights alone, around the attention's bare K/V stream floor (kind 2),
+// at one sequence and position pos.
+constexpr int kFloorBlock = 3;
+int launch_block_floor(leap_hip_attention *h, int layer, int pos, hipStream_t stream)
+{
+    const int li = layer - h->cfg.layer_begin;
+    if (h->w_fmt == 0 || !h->w_set[li]) return set_err(h, -EINVAL, "no weights set for layer %d", layer);
+    const int dim = h->q_dim, kv = h->kv_dim;
+    const int rows_qkv = dim + 2 * kv;
+    float *sink = h->out_dev;
+    if (h->w_fmt == 2) {
+        const int gs = h->gs;
+        for (int pass = 0; pass < 2; pass++) {
+            if (pass == 1)
+                if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, nullptr, nullptr, nullptr, sink, stream,
+                                    kFloorStream))
+                    return rc;
+            const int rows = pass == 0 ? rows_qkv : dim;
+            int rpt = 0;
+            Q8Fn floor = nullptr;
+            if (!pick_q8(dim, gs, pass == 0 ? leap::kQ8InRms : leap::kQ8InF32, rows, h->n_cu, &rpt, &floor) || !floor)
+                return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
+            leap::Q8Args qa{};
+            qa.w = pass == 0 ? h->w8_qkv + (size_t)li * rows_qkv * dim : h->w8_o + (size_t)li * dim * dim;
+            qa.ws = pass == 0 ? h->s8_qkv + (size_t)li * rows_qkv * (dim / gs) : h->s8_o + (size_t)li * dim * (dim / gs);
+            qa.rows = rows;
+            qa.out0 = sink;
+            const int per_wg = leap::kQ8Teams * rpt;
+            HIP_TRY(h, launch_k(floor, dim3((unsigned)((rows + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, qa));
+        }
+        return 0;
+    }
+    QkvFn qkv;
+    ProjFn proj;
+    GemvFloorFn floor = nullptr;
+    int rb;
+    if (!pick_proj(dim, &qkv, &proj, &rb, &floor))
+        return set_err(h, -EINVAL, "dim %d: the projections need dim in {2048, 3072, 4096, 5120, 8192}", dim);
+    HIP_TRY(h, launch_k(floor, dim3((unsigned)((rows_qkv + rb - 1) / rb)), dim3(leap::kGemvThreads), stream,
+                        (const float *)(h->w_qkv + (size_t)li * rows_qkv * dim), rows_qkv, sink));
+    if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, nullptr, nullptr, nullptr, sink, stream, kFloorStream))
+        return rc;
+    HIP_TRY(h, launch_k(floor, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), stream,
+                        (const float *)(h->w_o + (size_t)li * dim * dim), dim, sink));
+    return 0;
+}
+
 // x: the residual stream the q/k/v projection normalises; x_res: where the
 // wo product is added (x itself, or a device-accessible host copy of it).
 int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_res, hipStream_t stream)
@@ -1327,7 +1376,8 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
                                    int max_pos, long long total_rows, void *stream)
 {
     if (!h) return -EINVAL;
-    if (kind != kFloorLaunch && kind != kFloorStream) return set_err(h, -EINVAL, "floor kind %d is not 1 or 2", kind);
+    if (kind != kFloorLaunch && kind != kFloorStream && kind != kFloorBlock)
+        return set_err(h, -EINVAL, "floor kind %d is not 1, 2 or 3", kind);
     if (int rc = check_layer(h, layer)) return rc;
     if (n_seq <= 0 || n_seq > h->cfg.max_batch)
         return set_err(h, -EINVAL, "n_seq %d outside [1, %d]", n_seq, h->cfg.max_batch);
@@ -1336,6 +1386,12 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
     if (total_rows <= 0 || total_rows > (long long)n_seq * (max_pos + 1))
         return set_err(h, -EINVAL, "total_rows %lld outside [1, %lld]", total_rows, (long long)n_seq * (max_pos + 1));
     if (reinterpret_cast<uintptr_t>(pos) % 4) return set_err(h, -EINVAL, "pos must be 4-byte aligned");
+    if (kind == kFloorBlock) {
+        if (n_seq != 1 || pos || total_rows != (long long)max_pos + 1)
+            return set_err(h, -EINVAL, "the sub-block floor takes one sequence at max_pos (pos NULL)");
+        HIP_TRY(h, hipSetDevice(h->cfg.device));
+        return launch_block_floor(h, layer, max_pos, (hipStream_t)stream);
+    }
     if (spreads(shape_of(h), n_seq, total_rows))
         return set_err(h, -EINVAL,
                        "%d sequences of %d KV heads and %lld rows spread over the XCDs in the step; the floor "

@@ -131,3 +131,35 @@ def test_floor_launches_write_nothing(kind):
             att.floor_async(kind, 0, 1, 8191, 8192, s.cuda_stream)
         assert "spread" in str(ei.value)
         s.synchronize()
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_block_floor_launches_write_nothing(q8):
+    """Floor kind 3, the sub-block's floor (both projections streaming their
+    weights alone around the attention's bare K/V stream), for fp32 and
+    int8 weights: runs, changes neither the cache nor the block's buffers,
+    and refuses a layer without weights or a batch."""
+    import torch
+    from tests.helpers import block_inputs
+    nh, nkv, hd, T, gs = 16, 4, 128, 512, 64
+    dim = nh * hd
+    rng = rng_for(94, int(q8))
+    with HipAttention(nh, nkv, hd, T, n_layers=2) as att:
+        att.kv_fill_normal(94, 1.0 / np.sqrt(hd))
+        _, rms, *wf = block_inputs(rng, dim, nkv * hd)
+        if q8:
+            from oracle import oracle as O
+            att.set_layer_weights_q8(0, gs, rms, *(O.quantize_weight(w, gs) for w in wf))
+        else:
+            att.set_layer_weights(0, rms, *wf)
+        k0, v0 = att.kv_download(0, 0, 0, T)
+        s = torch.cuda.Stream()
+        for _ in range(3):
+            att.floor_async(3, 0, 1, T - 1, T, s.cuda_stream)
+        s.synchronize()
+        k1, v1 = att.kv_download(0, 0, 0, T)
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+        with pytest.raises(LeapError):  # no weights at layer 1
+            att.floor_async(3, 1, 1, T - 1, T, s.cuda_stream)
+        with pytest.raises(LeapError):  # one sequence only
+            att.floor_async(3, 0, 2, T - 1, 2 * T, s.cuda_stream)
