@@ -558,8 +558,8 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     __shared__ __align__(16) float p_lds[NW][R * G];
     __shared__ float4 q_lds[G][HD / 4];  // rotated, scaled q of the group's heads
     __shared__ float4 comb_o[NW][RPV][G][D4];
-    __shared__ float comb_l[NW][G];
-    __shared__ float comb_m[NW][G];
+    __shared__ __align__(16) float comb_l[G][NW];  // [head][wave]: a head's NW values in one read
+    __shared__ __align__(16) float comb_m[G][NW];
     __shared__ float2 ml_lds[GM * kFinalMax];  // the asymmetric merge's final (max, sum) pairs
     __shared__ int s_last;
 
@@ -884,8 +884,8 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     for (int h = 0; h < G; h++) {
         const float lw = score_rows_sum(l_run[h]);
         if (lane == 0) {
-            comb_l[wave][h] = lw;
-            comb_m[wave][h] = m_ref[h];
+            comb_l[h][wave] = lw;
+            comb_m[h][wave] = m_ref[h];
         }
     }
     __syncthreads();
@@ -913,17 +913,30 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     const __amdgpu_buffer_rsrc_t wm_rsrc = make_rsrc(a.ws_ml + ws_head0, ws_ml_bytes);
     for (int idx = tid; idx < G * D4; idx += S::THREADS) {
         const int ch = idx / D4, cd4 = idx % D4;  // head, float4 column
+        // Every LDS read of this thread as one batch ahead of the arithmetic:
+        // left to the compiler, two reads were in flight at a time between
+        // the fused multiply-adds, one LDS round trip per wave's partial.
+        float mw[NW], lw[NW];
+        float4 ow[NW][RPV];
+#pragma unroll
+        for (int w = 0; w < NW; w++) mw[w] = comb_m[ch][w];
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int r = 0; r < RPV; r++) ow[w][r] = comb_o[w][r][ch][cd4];
+#pragma unroll
+        for (int w = 0; w < NW; w++) lw[w] = comb_l[ch][w];
+        __builtin_amdgcn_sched_barrier(0);
         float M = -INFINITY, L = 0.f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, comb_m[w][ch]);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, mw[w]);
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float mw = comb_m[w][ch];
-            const float sc = (mw == -INFINITY) ? 0.0f : fast_exp2(mw - M);
+            const float sc = (mw[w] == -INFINITY) ? 0.0f : fast_exp2(mw[w] - M);
 #pragma unroll
-            for (int r = 0; r < RPV; r++) fma4(o, sc, comb_o[w][r][ch][cd4]);
-            L += sc * comb_l[w][ch];
+            for (int r = 0; r < RPV; r++) fma4(o, sc, ow[w][r]);
+            L += sc * lw[w];
         }
         if (single) {
             emit(ch, cd4, o, M, L);
