@@ -57,6 +57,34 @@ constexpr int kHelpMinRecords = 32;       // records from which two workgroups s
 constexpr int kSc1 = 16;                  // cache policy sc1 (device scope): miss in L1, read L2
 constexpr int kNt = 2;                    // cache policy nt: streamed once (the K/V rows of a step)
 
+// Division by a launch constant d >= 1 of numerators n < 2^31, as a
+// multiply-high and a shift (Granlund and Montgomery, "Division by Invariant
+// Integers using Multiplication", PLDI 1994, section 4, figure 4.1): with
+// s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1 < 2^32,
+// n / d = (mulhi(n, m) + n) >> s, and mulhi(n, m) + n < 2n does not wrap.
+// The host computes (m, s) once per launch, so that the prologue's
+// quotients (workgroup id to chunk and group, group to sequence, positions
+// to chunks) take three scalar instructions each instead of a reciprocal
+// on the vector unit, its move back to a scalar register and the
+// correction steps, which lie on the path to the first loads.
+struct FastDiv {
+    uint32_t m, s;
+};
+__host__ __device__ constexpr FastDiv make_fastdiv(uint32_t d)
+{
+    uint32_t s = 0;
+    while ((1ull << s) < d) s++;
+    return FastDiv{(uint32_t)((((1ull << s) - d) << 32) / d + 1), s};
+}
+__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f)
+{
+#ifdef __HIP_DEVICE_COMPILE__
+    return (__umulhi(n, f.m) + n) >> f.s;
+#else
+    return (uint32_t)((((uint64_t)n * f.m) >> 32) + n) >> f.s;
+#endif
+}
+
 // Partial records per head of a launch with grid_chunks chunks per sequence:
 // one per chunk, then one per first-level sub-group.
 __host__ __device__ constexpr int records_per_head(int grid_chunks)
@@ -117,6 +145,8 @@ struct StepArgs {
                          // prologue reads first keep their offsets
     float *ws_po;        // [n_groups << spread_log2][G][HD] each part's unnormalised output
     float2 *ws_pml;      // [n_groups << spread_log2][G] its (max, sum), log2 units
+    FastDiv by_grid_chunks, by_kv_heads, by_chunk, by_even;  // divisions by grid_chunks, n_kv_heads,
+                                                              // chunk and even_chunks (1 if 0)
     int kv_split;        // 1: n_kv_heads counts each of the cache's n_kv_heads / 2 heads twice, as
                          // two groups of G q heads (kv_group); 0: one group per head
 #ifdef LEAP_TIMELINE
@@ -221,12 +251,14 @@ __host__ __device__ constexpr bool part_launch(int even_chunks, int chunk, int p
 // (one 32-bit quotient per sequence, ahead of the first loads).
 __device__ __forceinline__ int seq_chunks(const StepArgs &a, int T)
 {
-    return a.even_chunks > 0 ? min(a.even_chunks, T) : (T + a.chunk - 1) / a.chunk;
+    return a.even_chunks > 0 ? min(a.even_chunks, T) : (int)fast_div((uint32_t)(T + a.chunk - 1), a.by_chunk);
 }
 __device__ __forceinline__ int chunk_start(const StepArgs &a, int T, int n_chunks, int c)
 {
     if (a.even_chunks > 0) {
-        const unsigned q = (unsigned)T / (unsigned)n_chunks, r = (unsigned)T - q * (unsigned)n_chunks;
+        // n_chunks = min(even_chunks, T): T / even_chunks, or 1 when T < even_chunks
+        const unsigned q = T >= a.even_chunks ? fast_div((uint32_t)T, a.by_even) : 1u;
+        const unsigned r = (unsigned)T - q * (unsigned)n_chunks;
         return (int)((unsigned)c * q + min((unsigned)c, r));
     }
     return min(c * a.chunk, T);
@@ -485,24 +517,26 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     asm volatile("" ::"s"(a.q), "s"(a.k_new), "s"(a.v_new), "s"(a.k_cache), "s"(a.v_cache), "s"(a.rope),
                  "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar), "s"(a.max_pos), "s"(a.seq_len),
                  "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks), "s"(a.n_groups),
-                 "s"(a.spread_log2), "s"(a.even_chunks));
+                 "s"(a.spread_log2), "s"(a.even_chunks), "s"(a.by_grid_chunks.m), "s"(a.by_grid_chunks.s),
+                 "s"(a.by_kv_heads.m), "s"(a.by_kv_heads.s), "s"(a.by_chunk.m), "s"(a.by_chunk.s));
     // id = ((pg / 8) * grid_chunks + lc) * 8 + pg % 8, where the part-group
     // pg = group * 2^spread_log2 + part covers the group's chunks
     // [part * grid_chunks, (part + 1) * grid_chunks) and lc is the chunk
     // within the part.  Every workgroup of a part-group runs on one XCD.
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
-    const int lc = local % a.grid_chunks;
-    const int pgroup = (local / a.grid_chunks) * kXcds + xcd;
+    const int lq = (int)fast_div((uint32_t)local, a.by_grid_chunks);
+    const int lc = local - lq * a.grid_chunks;
+    const int pgroup = lq * kXcds + xcd;
     if (pgroup >= (a.n_groups << a.spread_log2)) return;
     const int group = pgroup >> a.spread_log2;
     const int part = pgroup & ((1 << a.spread_log2) - 1);
     const int chunk_id = part * a.grid_chunks + lc;  // within the group
-    const int seq = group / a.n_kv_heads;
+    const int seq = (int)fast_div((uint32_t)group, a.by_kv_heads);
+    const int kvv = group - seq * a.n_kv_heads;  // the group within its sequence
     // KVS: two launch groups per cache head (kv_split set), compiled as
     // instances of their own so that the others keep their code
-    const KvGroup kg = KVS ? kv_group<G>(group % a.n_kv_heads, a.n_kv_heads, 1)
-                           : KvGroup{group % a.n_kv_heads, 0, (group % a.n_kv_heads) * G};
+    const KvGroup kg = KVS ? kv_group<G>(kvv, a.n_kv_heads, 1) : KvGroup{kvv, 0, kvv * G};
     const int kvh = kg.kvh;
     const bool store_new = kg.half == 0;  // the one group per cache head that appends the new token
     const int tid = threadIdx.x;
@@ -521,7 +555,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
         return;
     }
     const int T = pos + 1;
-    const int n_chunks = PART ? seq_chunks(a, T) : (T + a.chunk - 1) / a.chunk;
+    const int n_chunks = PART ? seq_chunks(a, T) : (int)fast_div((uint32_t)(T + a.chunk - 1), a.by_chunk);
     if (chunk_id >= n_chunks) return;
     // chunks of this part (at least 1 here)
     const int n_local = min(a.grid_chunks, n_chunks - part * a.grid_chunks);
@@ -1416,14 +1450,17 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
     // the argument block as one batch of loads, as in the decode kernel
     asm volatile("" ::"s"(a.k_cache), "s"(a.v_cache), "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar),
                  "s"(a.max_pos), "s"(a.seq_len), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
-                 "s"(a.n_groups), "s"(a.even_chunks), "s"(a.kv_split));
+                 "s"(a.n_groups), "s"(a.even_chunks), "s"(a.kv_split), "s"(a.by_grid_chunks.m),
+                 "s"(a.by_grid_chunks.s), "s"(a.by_kv_heads.m), "s"(a.by_kv_heads.s), "s"(a.by_chunk.m),
+                 "s"(a.by_chunk.s));
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
-    const int chunk_id = local % a.grid_chunks;
-    const int group = (local / a.grid_chunks) * kXcds + xcd;
+    const int lq = (int)fast_div((uint32_t)local, a.by_grid_chunks);
+    const int chunk_id = local - lq * a.grid_chunks;
+    const int group = lq * kXcds + xcd;
     if (group >= a.n_groups) return;
-    const int seq = group / a.n_kv_heads;
-    const int kvh = kv_group<G>(group % a.n_kv_heads, a.n_kv_heads, a.kv_split).kvh;
+    const int seq = (int)fast_div((uint32_t)group, a.by_kv_heads);
+    const int kvh = kv_group<G>(group - seq * a.n_kv_heads, a.n_kv_heads, a.kv_split).kvh;
     const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
     if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
     const int T = pos + 1;

@@ -410,6 +410,10 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     a.scale_log2 = (float)(1.4426950408889634 / std::sqrt((double)hd));
 
     a.spread_log2 = spread_log2;
+    a.by_grid_chunks = leap::make_fastdiv((uint32_t)grid_x);
+    a.by_kv_heads = leap::make_fastdiv((uint32_t)s.n_kv_heads);
+    a.by_chunk = leap::make_fastdiv((uint32_t)chunk);
+    a.by_even = leap::make_fastdiv(even > 0 ? (uint32_t)even : 1u);
     a.kv_split = s.kv_split;
 #ifdef LEAP_TIMELINE
     a.tl = (g_tl_ring && kind == kDecode)
