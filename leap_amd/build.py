@@ -31,6 +31,10 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast-honor-pragmas",
+    # the decode kernel's leading 14 argument words arrive preloaded in
+    # scalar registers (kernels whose first argument is a struct preload
+    # nothing)
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
 ]
 
 

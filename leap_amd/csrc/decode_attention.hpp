@@ -154,6 +154,62 @@ struct StepArgs {
 #endif
 };
 
+// The decode kernel's (and its floor kernels') leading arguments: 14 words
+// that the dispatch preloads into scalar registers (the library is built
+// with -mllvm -amdgpu-kernarg-preload-count=14; the code object carries a
+// fallback that loads them itself where the firmware does not preload).
+// They hold everything the prologue needs up to the first tile's loads
+// when a launch serves one sequence at a host position, so that those
+// loads do not wait for a load of the argument block (about 0.25 us on an
+// idle chip); the argument block (StepArgs) follows in the kernel
+// arguments and is read after they are issued.  Launches of several
+// sequences or with positions on the device set w1 = kPreGeneral and read
+// their prologue from the argument block.
+struct Preload {
+    const float *q;      // StepArgs::q
+    const float *k_new;  // StepArgs::k_new
+    float *k_cache;      // StepArgs::k_cache
+    float *v_cache;      // StepArgs::v_cache
+    const float4 *rope;  // StepArgs::rope
+    uint32_t m_gc;       // StepArgs::by_grid_chunks.m
+    uint32_t w0;         // grid_chunks | by_grid_chunks.s << 10 | spread_log2 << 14 | n_kv_heads << 16
+    uint32_t w1;         // one sequence at a host position: pos | n_chunks << 21; else kPreGeneral
+    uint32_t w2;         // the chunks: chunk c starts at min(c q + min(c, r), T), w2 = q | r << 21
+};
+constexpr uint32_t kPreGeneral = 0xFFFFFFFFu;
+// The kernels take the words as leading scalar parameters (only those are
+// preloaded), in Preload's order, ahead of the argument block.
+#define LEAP_PRELOAD_PARAMS                                                                                  \
+    const float *pre_q, const float *pre_k_new, float *pre_k_cache, float *pre_v_cache,                      \
+        const float4 *pre_rope, uint32_t pre_m_gc, uint32_t pre_w0, uint32_t pre_w1, uint32_t pre_w2
+#define LEAP_PRELOAD                                                                                         \
+    Preload { pre_q, pre_k_new, pre_k_cache, pre_v_cache, pre_rope, pre_m_gc, pre_w0, pre_w1, pre_w2 }
+constexpr uint32_t kPreLimit = 1u << 21;  // pos, q < kPreLimit and n_chunks, r < 2^11 for the packed words
+// StepArgs' byte offset in the kernel arguments, after the preloaded words
+constexpr unsigned kArgsOffset = 5 * sizeof(void *) + 4 * sizeof(uint32_t);
+static_assert(kArgsOffset == 56 && alignof(StepArgs) <= 8, "argument layout");
+
+// The preloaded words of a launch (host side): the launch constants, and
+// the positions' words when it serves one sequence at host position pos
+// (one_seq), with chunk rows `chunk`, or even_chunks near-equal chunks.
+inline Preload make_preload(const StepArgs &a, bool one_seq)
+{
+    Preload p{a.q, a.k_new, a.k_cache, a.v_cache, a.rope, a.by_grid_chunks.m, 0u, kPreGeneral, 0u};
+    p.w0 = (uint32_t)a.grid_chunks | (a.by_grid_chunks.s << 10) | ((uint32_t)a.spread_log2 << 14) |
+           ((uint32_t)a.n_kv_heads << 16);
+    const int T = a.pos_scalar + 1;
+    if (!one_seq || a.pos_dev || a.pos_scalar < 0 || a.pos_scalar >= a.seq_len || a.pos_scalar > a.max_pos ||
+        (uint32_t)a.pos_scalar >= kPreLimit)
+        return p;  // the kernel checks the position (and writes NaN rows for one it cannot serve)
+    const int n_chunks = a.even_chunks > 0 ? (T < a.even_chunks ? T : a.even_chunks) : (T + a.chunk - 1) / a.chunk;
+    const int q = a.even_chunks > 0 ? T / n_chunks : a.chunk;
+    const int r = a.even_chunks > 0 ? T % n_chunks : 0;
+    if ((uint32_t)q >= kPreLimit || n_chunks >= 2048) return p;
+    p.w1 = (uint32_t)a.pos_scalar | ((uint32_t)n_chunks << 21);
+    p.w2 = (uint32_t)q | ((uint32_t)r << 21);
+    return p;
+}
+
 // ---- timeline (measurement build only) --------------------------------------
 //
 // Built with -DLEAP_TIMELINE (`python -m leap_amd.build` builds that library
@@ -504,90 +560,117 @@ __device__ __forceinline__ int fold_helper_wait(int *ctr, int target, int mode)
 }
 
 template <int HD, int G, int NW, bool MFMA, bool PART, bool KVS>
-__device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timeline &tl)
+__device__ __forceinline__ void decode_attention_body(const StepArgs &args, const Preload &pre, Timeline &tl)
 {
     using S = Shape<HD, G, NW>;
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
     constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, GM = S::GM, MG = S::MG;
 
-    // The argument block's fields that the prologue reads, loaded as one
-    // batch before the first branch (an empty asm that takes them as
-    // inputs): left to the compiler, each load follows the branch that first
-    // needs it, one dependent round trip after another.
-    asm volatile("" ::"s"(a.q), "s"(a.k_new), "s"(a.v_new), "s"(a.k_cache), "s"(a.v_cache), "s"(a.rope),
-                 "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar), "s"(a.max_pos), "s"(a.seq_len),
-                 "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks), "s"(a.n_groups),
-                 "s"(a.spread_log2), "s"(a.even_chunks), "s"(a.by_grid_chunks.m), "s"(a.by_grid_chunks.s),
-                 "s"(a.by_kv_heads.m), "s"(a.by_kv_heads.s), "s"(a.by_chunk.m), "s"(a.by_chunk.s));
     // id = ((pg / 8) * grid_chunks + lc) * 8 + pg % 8, where the part-group
     // pg = group * 2^spread_log2 + part covers the group's chunks
     // [part * grid_chunks, (part + 1) * grid_chunks) and lc is the chunk
     // within the part.  Every workgroup of a part-group runs on one XCD.
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
-    const int lq = (int)fast_div((uint32_t)local, a.by_grid_chunks);
-    const int lc = local - lq * a.grid_chunks;
+    const int grid_chunks = (int)(pre.w0 & 1023u);
+    const int spread_log2 = (int)((pre.w0 >> 14) & 3u);
+    const int n_kv_heads = (int)(pre.w0 >> 16);
+    const int lq = (int)fast_div((uint32_t)local, FastDiv{pre.m_gc, (pre.w0 >> 10) & 15u});
+    const int lc = local - lq * grid_chunks;
     const int pgroup = lq * kXcds + xcd;
-    if (pgroup >= (a.n_groups << a.spread_log2)) return;
-    const int group = pgroup >> a.spread_log2;
-    const int part = pgroup & ((1 << a.spread_log2) - 1);
-    const int chunk_id = part * a.grid_chunks + lc;  // within the group
-    const int seq = (int)fast_div((uint32_t)group, a.by_kv_heads);
-    const int kvv = group - seq * a.n_kv_heads;  // the group within its sequence
+    const int group = pgroup >> spread_log2;
+    const int part = pgroup & ((1 << spread_log2) - 1);
+    const int chunk_id = part * grid_chunks + lc;  // within the group
+    // The sequence, its position, its chunks (chunk c starts at
+    // min(c cq + min(c, cr), T)) and its slab: from the preloaded words for
+    // one sequence at a host position, else from the argument block, whose
+    // fields are loaded as one batch before the first branch there (an
+    // empty asm that takes them as inputs): left to the compiler, each load
+    // follows the branch that first needs it, one dependent round trip
+    // after another.
+    int seq, pos, n_chunks, cq, cr;
+    size_t slab;
+    if (pre.w1 != kPreGeneral) {
+        if (group >= n_kv_heads) return;
+        seq = 0;
+        pos = (int)(pre.w1 & (kPreLimit - 1));
+        n_chunks = (int)(pre.w1 >> 21);
+        cq = (int)(pre.w2 & (kPreLimit - 1));
+        cr = (int)(pre.w2 >> 21);
+        slab = 0;
+    } else {
+        asm volatile("" ::"s"(args.pos_dev), "s"(args.seq_stride), "s"(args.pos_scalar), "s"(args.max_pos),
+                     "s"(args.seq_len), "s"(args.n_heads), "s"(args.chunk), "s"(args.n_groups),
+                     "s"(args.even_chunks), "s"(args.by_kv_heads.m), "s"(args.by_kv_heads.s), "s"(args.by_chunk.m),
+                     "s"(args.by_chunk.s), "s"(args.by_even.m), "s"(args.by_even.s), "s"(args.out));
+        if (pgroup >= (args.n_groups << spread_log2)) return;
+        seq = (int)fast_div((uint32_t)group, args.by_kv_heads);
+        pos = args.pos_dev ? args.pos_dev[seq] : args.pos_scalar;
+        if (pos < 0 || pos >= args.seq_len || pos > args.max_pos) {
+            // A device position the launch cannot serve: no row is read or
+            // written, and the sequence's output rows read NaN so that the
+            // skip is visible (the first chunk of each group writes its
+            // heads; a spread launch's merge launch does it instead).
+            const int kvv = group - seq * n_kv_heads;
+            const int qh0 = KVS ? kv_group<G>(kvv, n_kv_heads, 1).qh0 : kvv * G;
+            if (chunk_id == 0 && spread_log2 == 0)
+                for (int i = threadIdx.x; i < G * HD; i += NW * kWave)
+                    args.out[(size_t)seq * args.n_heads * HD + (size_t)qh0 * HD + i] = __builtin_nanf("");
+            return;
+        }
+        const int T = pos + 1;
+        n_chunks = PART ? seq_chunks(args, T) : (int)fast_div((uint32_t)(T + args.chunk - 1), args.by_chunk);
+        if (args.even_chunks > 0) {
+            // n_chunks = min(even_chunks, T): T / even_chunks, or 1 when T < even_chunks
+            cq = T >= args.even_chunks ? (int)fast_div((uint32_t)T, args.by_even) : 1;
+            cr = T - cq * n_chunks;
+        } else {
+            cq = args.chunk;
+            cr = 0;
+        }
+        slab = (size_t)seq * (size_t)args.seq_stride;
+    }
+    const int kvv = group - seq * n_kv_heads;  // the group within its sequence
     // KVS: two launch groups per cache head (kv_split set), compiled as
     // instances of their own so that the others keep their code
-    const KvGroup kg = KVS ? kv_group<G>(kvv, a.n_kv_heads, 1) : KvGroup{kvv, 0, kvv * G};
+    const KvGroup kg = KVS ? kv_group<G>(kvv, n_kv_heads, 1) : KvGroup{kvv, 0, kvv * G};
     const int kvh = kg.kvh;
     const bool store_new = kg.half == 0;  // the one group per cache head that appends the new token
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
 
-    const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
-    if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) {
-        // A device position the launch cannot serve: no row is read or
-        // written, and the sequence's output rows read NaN so that the
-        // skip is visible (the first chunk of each group writes its heads;
-        // a spread launch's merge launch does it instead).
-        if (chunk_id == 0 && a.spread_log2 == 0)
-            for (int i = threadIdx.x; i < G * HD; i += NW * kWave)
-                a.out[(size_t)seq * a.n_heads * HD + (size_t)kg.qh0 * HD + i] = __builtin_nanf("");
-        return;
-    }
     const int T = pos + 1;
-    const int n_chunks = PART ? seq_chunks(a, T) : (int)fast_div((uint32_t)(T + a.chunk - 1), a.by_chunk);
     if (chunk_id >= n_chunks) return;
     // chunks of this part (at least 1 here)
-    const int n_local = min(a.grid_chunks, n_chunks - part * a.grid_chunks);
+    const int n_local = min(grid_chunks, n_chunks - part * grid_chunks);
 
-    const int kv_dim = (KVS ? a.n_kv_heads / 2 : a.n_kv_heads) * HD;
-    const int q_dim = a.n_heads * HD;
+    const int kv_dim = (KVS ? n_kv_heads / 2 : n_kv_heads) * HD;
+    const int q_dim = n_kv_heads * G * HD;  // every q head of a sequence
     const uint32_t row_bytes = (uint32_t)kv_dim * 4u;
-    const size_t slab = (size_t)seq * (size_t)a.seq_stride;
-    float *kc = a.k_cache + slab + (size_t)kvh * HD;
-    float *vc = a.v_cache + slab + (size_t)kvh * HD;
+    float *kc = pre.k_cache + slab + (size_t)kvh * HD;
+    float *vc = pre.v_cache + slab + (size_t)kvh * HD;
     // This chunk's rows [chunk_begin, last].  With PART a pass may reach past
     // the chunk's end.  Rows up to min(pos, chunk end) of this KV head are in
     // range: row pos (the new token, from registers) and the rows beyond
     // read 0 without touching memory, and their scores are masked.
     int chunk_begin, chunk_end, row_end, last;
     if constexpr (PART) {
-        chunk_begin = chunk_start(a, T, n_chunks, chunk_id);
-        chunk_end = chunk_start(a, T, n_chunks, chunk_id + 1);
+        chunk_begin = min(chunk_id * cq + min(chunk_id, cr), T);
+        chunk_end = min((chunk_id + 1) * cq + min(chunk_id + 1, cr), T);
         row_end = min(pos, chunk_end);
         last = min(pos, chunk_end - 1);
     } else {
-        chunk_begin = chunk_id * a.chunk;
-        chunk_end = min(chunk_begin + a.chunk, T);
+        chunk_begin = chunk_id * cq;
+        chunk_end = min(chunk_begin + cq, T);
         row_end = pos;
         last = pos;
     }
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc, (uint32_t)row_end * row_bytes);
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)row_end * row_bytes);
-    const float *k_row_new = a.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
-    const float *v_row_new = a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
-    const float *qg = a.q + (size_t)seq * q_dim + (size_t)kg.qh0 * HD;
-    const float4 *rope_row = a.rope + (size_t)pos * (HD / 4);
+    const float *k_row_new = pre.k_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
+    const float *qg = pre.q + (size_t)seq * q_dim + (size_t)kg.qh0 * HD;
+    const float4 *rope_row = pre.rope + (size_t)pos * (HD / 4);
 
     __shared__ __align__(16) float p_lds[NW][R * G];
     __shared__ float4 q_lds[G][HD / 4];  // rotated, scaled q of the group's heads
@@ -615,7 +698,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     // pos loads and rotates the new token's k and v.
     // passes over this chunk's rows that reach a position <= pos
     const int n_sub = PART ? (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS
-                           : (min(a.chunk, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
+                           : (min(cq, T - chunk_begin) + S::ROWS - 1) / S::ROWS;
     const bool has_pos = (chunk_id == n_chunks - 1);
     constexpr int PAIRS = G * HD / 2;
     constexpr int QP = (PAIRS + S::THREADS - 1) / S::THREADS;  // q pairs per thread
@@ -653,15 +736,15 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     // spelled out, so that the rounding does not depend on which product the
     // compiler would have fused.
     float *q_flat = reinterpret_cast<float *>(&q_lds[0][0]);
-    auto rotate_q = [&]() {
+    auto rotate_q = [&](float scale_log2) {
 #pragma clang fp contract(off)
 #pragma unroll
         for (int i = 0; i < QP; i++) {
             const int pair = tid + i * S::THREADS;
             if (pair < PAIRS) {
                 const float x0 = qp[i].x, x1 = qp[i].y, c = qt[i].x, sn = qt[i].y;
-                q_flat[2 * pair] = __builtin_fmaf(x0, c, -(x1 * sn)) * a.scale_log2;
-                q_flat[2 * pair + 1] = __builtin_fmaf(x0, sn, x1 * c) * a.scale_log2;
+                q_flat[2 * pair] = __builtin_fmaf(x0, c, -(x1 * sn)) * scale_log2;
+                q_flat[2 * pair + 1] = __builtin_fmaf(x0, sn, x1 * c) * scale_log2;
             }
         }
     };
@@ -677,7 +760,6 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     // of the v row across lanes.
     const uint32_t new_bytes = has_pos ? (uint32_t)HD * 4u : 0u;
     const __amdgpu_buffer_rsrc_t kn_rsrc = make_rsrc(k_row_new, new_bytes);
-    const __amdgpu_buffer_rsrc_t vn_rsrc = make_rsrc(v_row_new, new_bytes);
     // (scheduling barriers keep the compiler from reordering the groups)
     // With PART, passes start at pass chunk_id mod n_sub and wrap around.
     // A launch's chunks start at equal strides, and when the stride is a
@@ -696,9 +778,28 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     load_k(sub0);
     __builtin_amdgcn_sched_barrier(0);
     load_v(sub0);
+    __builtin_amdgcn_sched_barrier(0);
+    // The argument block, from here on: loaded through a copy of the
+    // kernel-argument pointer that the compiler cannot see through, so that
+    // none of its loads (or a wait for one) is placed ahead of the loads
+    // above.
+#ifdef __HIP_DEVICE_COMPILE__
+    auto kargs = __builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kargs));
+    typedef __attribute__((address_space(4))) const StepArgs KernargStepArgs;
+    typedef __attribute__((address_space(4))) const char KernargBytes;
+    const StepArgs a = *(KernargStepArgs *)((KernargBytes *)kargs + kArgsOffset);
+#else
+    const StepArgs &a = args;
+#endif
+    // every field the rest reads, as one batch of loads
+    asm volatile("" ::"s"(a.v_new), "s"(a.scale_log2), "s"(a.out), "s"(a.ws_o), "s"(a.ws_ml), "s"(a.counters),
+                 "s"(a.merge_asym), "s"(a.ws_po), "s"(a.ws_pml));
+    const float *v_row_new = a.v_new + (size_t)seq * kv_dim + (size_t)kvh * HD;
+    const __amdgpu_buffer_rsrc_t vn_rsrc = make_rsrc(v_row_new, new_bytes);
     const float4 vnew_l = buf_load4(vn_rsrc, 16u * (uint32_t)lane);
     __builtin_amdgcn_sched_barrier(0);
-    rotate_q();
+    rotate_q(a.scale_log2);
     // The table row, for the new token's k, in this wave's combine buffer
     // (unused until the waves combine): float4 [D4, 2*D4); the k_new row
     // goes to [0, D4) when it is needed.
@@ -927,11 +1028,11 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
 
     // Combine the waves: one float4 of one head per thread.
     const bool single = (n_local == 1);
-    const int n_rec = records_per_head(a.grid_chunks);
+    const int n_rec = records_per_head(grid_chunks);
     const size_t ws_head0 = (size_t)pgroup * G * (size_t)n_rec;
     // A part-group's finished result: the output row (one part), or the
     // part's unnormalised record for the cross-XCD merge launch.
-    const bool parts = a.spread_log2 > 0;
+    const bool parts = spread_log2 > 0;
     auto emit = [&](int head, int col, float4 o, float M, float L) {
         if (parts) {
             reinterpret_cast<float4 *>(a.ws_po + ((size_t)pgroup * G + head) * HD)[col] = o;
@@ -1191,7 +1292,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
             }
         }
     };
-    int *ctr = a.counters + (size_t)pgroup * (size_t)counters_per_group(a.grid_chunks);
+    int *ctr = a.counters + (size_t)pgroup * (size_t)counters_per_group(grid_chunks);
 
     // The fold of a one-level merge's records [first, first + n_rt) (n_c a
     // compile-time bound), after this workgroup counted in with result prev.
@@ -1346,7 +1447,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
         return;
     }
     if (mg == 0 && live) {
-        const uint32_t row = (uint32_t)(mh * n_rec + a.grid_chunks + sg);
+        const uint32_t row = (uint32_t)(mh * n_rec + grid_chunks + sg);
         buf_store4(wo_rsrc, row * (HD * 4u) + 16u * md4, ox);
         if (md4 == 0) buf_store2(wm_rsrc, row * 8u, make_float2(Mx, Lx));
     }
@@ -1364,17 +1465,17 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &a, Timelin
     if (!s_last) return;
     tl.role(kTlRoleFinal, n_sg - 1);
     if (tid == 0) ctr[0] = 0;
-    fold(a.grid_chunks, n_sg, ox, Mx, Lx);
+    fold(grid_chunks, n_sg, ox, Mx, Lx);
     if (mg == 0 && live) emit(mh, md4, ox, Mx, Lx);
     tl.mark(kTlFolded);
 }
 
 template <int HD, int G, int NW, bool MFMA = true, bool PART = false, bool KVS = false>
-__global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(StepArgs a)
+__global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(LEAP_PRELOAD_PARAMS, StepArgs a)
 {
     Timeline tl;
     tl.mark(kTlStart);
-    decode_attention_body<HD, G, NW, MFMA, PART, KVS>(a, tl);
+    decode_attention_body<HD, G, NW, MFMA, PART, KVS>(a, LEAP_PRELOAD, tl);
 #ifdef LEAP_TIMELINE
     tl.mark(kTlEnd);
     tl.flush(a.tl);
@@ -1426,10 +1527,11 @@ __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
 
 // ---- launch and stream floors (measurement only) ----------------------------
 //
-// Two kernels with the decode kernel's grid, block size and argument, for
-// measuring what any one-launch design at a given shape must pay:
+// Two kernels with the decode kernel's grid, block size and arguments (the
+// preloaded words and the argument block), for measuring what any
+// one-launch design at a given shape must pay:
 //   - floor_launch_kernel reads two kernel arguments and exits (the launch,
-//     the argument load and the drain of an empty grid);
+//     the preload and the drain of an empty grid);
 //   - floor_stream_kernel streams the same K and V rows with the same loads
 //     (128-bit, non-temporal, the same lane layout and passes) and only sums
 //     them (the launch plus the bare stream of the step's bytes).
@@ -1437,49 +1539,70 @@ __global__ __launch_bounds__(G * HD / 4) void part_merge_kernel(StepArgs a)
 // data never meets (a NaN with a particular payload).
 
 template <int HD, int G, int NW>
-__global__ __launch_bounds__(NW * kWave) void floor_launch_kernel(StepArgs a)
+__global__ __launch_bounds__(NW * kWave) void floor_launch_kernel(LEAP_PRELOAD_PARAMS, StepArgs a)
 {
-    if (a.grid_chunks < 0 && a.n_groups < 0) a.out[threadIdx.x] = 0.0f;
+    if (pre_w0 == 0u && pre_w1 == 0u) a.out[threadIdx.x] = 0.0f;
 }
 
-template <int HD, int G, int NW>
-__global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(StepArgs a)
+template <int HD, int G, int NW, bool KVS, bool PART>
+__global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(LEAP_PRELOAD_PARAMS, StepArgs a)
 {
     using S = Shape<HD, G, NW>;
     constexpr int NF = S::NF, R = S::R, KS = S::KS, LPV = S::LPV, RPV = S::RPV, VS = S::VS;
-    // the argument block as one batch of loads, as in the decode kernel
-    asm volatile("" ::"s"(a.k_cache), "s"(a.v_cache), "s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar),
-                 "s"(a.max_pos), "s"(a.seq_len), "s"(a.n_kv_heads), "s"(a.chunk), "s"(a.grid_chunks),
-                 "s"(a.n_groups), "s"(a.even_chunks), "s"(a.kv_split), "s"(a.by_grid_chunks.m),
-                 "s"(a.by_grid_chunks.s), "s"(a.by_kv_heads.m), "s"(a.by_kv_heads.s), "s"(a.by_chunk.m),
-                 "s"(a.by_chunk.s));
+    // The prologue as the decode kernel's: from the preloaded words for one
+    // sequence at a host position, else from the argument block.  (The
+    // floors run without a spread.)
     const int xcd = blockIdx.x % kXcds;
     const int local = blockIdx.x / kXcds;
-    const int lq = (int)fast_div((uint32_t)local, a.by_grid_chunks);
-    const int chunk_id = local - lq * a.grid_chunks;
+    const int grid_chunks = (int)(pre_w0 & 1023u);
+    const int n_kv_heads = (int)(pre_w0 >> 16);
+    const int lq = (int)fast_div((uint32_t)local, FastDiv{pre_m_gc, (pre_w0 >> 10) & 15u});
+    const int chunk_id = local - lq * grid_chunks;
     const int group = lq * kXcds + xcd;
-    if (group >= a.n_groups) return;
-    const int seq = (int)fast_div((uint32_t)group, a.by_kv_heads);
-    const int kvh = kv_group<G>(group - seq * a.n_kv_heads, a.n_kv_heads, a.kv_split).kvh;
-    const int pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
-    if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
+    int seq, pos, n_chunks, cq, cr;
+    size_t slab;
+    if (pre_w1 != kPreGeneral) {
+        if (group >= n_kv_heads) return;
+        seq = 0;
+        pos = (int)(pre_w1 & (kPreLimit - 1));
+        n_chunks = (int)(pre_w1 >> 21);
+        cq = (int)(pre_w2 & (kPreLimit - 1));
+        cr = (int)(pre_w2 >> 21);
+        slab = 0;
+    } else {
+        asm volatile("" ::"s"(a.pos_dev), "s"(a.seq_stride), "s"(a.pos_scalar), "s"(a.max_pos), "s"(a.seq_len),
+                     "s"(a.chunk), "s"(a.n_groups), "s"(a.even_chunks), "s"(a.by_kv_heads.m), "s"(a.by_kv_heads.s),
+                     "s"(a.by_chunk.m), "s"(a.by_chunk.s), "s"(a.by_even.m), "s"(a.by_even.s));
+        if (group >= a.n_groups) return;
+        seq = (int)fast_div((uint32_t)group, a.by_kv_heads);
+        pos = a.pos_dev ? a.pos_dev[seq] : a.pos_scalar;
+        if (pos < 0 || pos >= a.seq_len || pos > a.max_pos) return;
+        n_chunks = seq_chunks(a, pos + 1);
+        if (a.even_chunks > 0) {
+            cq = pos + 1 >= a.even_chunks ? (int)fast_div((uint32_t)(pos + 1), a.by_even) : 1;
+            cr = pos + 1 - cq * n_chunks;
+        } else {
+            cq = a.chunk;
+            cr = 0;
+        }
+        slab = (size_t)seq * (size_t)a.seq_stride;
+    }
+    const int kvh = kv_group<G>(group - seq * n_kv_heads, n_kv_heads, KVS ? 1 : 0).kvh;
     const int T = pos + 1;
-    const int n_chunks = seq_chunks(a, T);
     if (chunk_id >= n_chunks) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t row_bytes = (uint32_t)((a.n_kv_heads >> a.kv_split) * HD) * 4u;
-    const size_t slab = (size_t)seq * (size_t)a.seq_stride;
-    const int chunk_begin = chunk_start(a, T, n_chunks, chunk_id);
-    const int chunk_end = chunk_start(a, T, n_chunks, chunk_id + 1);
+    const uint32_t row_bytes = (uint32_t)((KVS ? n_kv_heads / 2 : n_kv_heads) * HD) * 4u;
+    const int chunk_begin = min(chunk_id * cq + min(chunk_id, cr), T);
+    const int chunk_end = min((chunk_id + 1) * cq + min(chunk_id + 1, cr), T);
     const uint32_t range = (uint32_t)min(pos, chunk_end) * row_bytes;  // as the step's
-    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(a.k_cache + slab + (size_t)kvh * HD, range);
-    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(a.v_cache + slab + (size_t)kvh * HD, range);
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(pre_k_cache + slab + (size_t)kvh * HD, range);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(pre_v_cache + slab + (size_t)kvh * HD, range);
     const int kj = lane & 3, ksl = (lane >> 2) & 7, kq = lane >> 5, krow = 4 * kq + kj;
     const int vg = lane / LPV, vj = lane % LPV;
     const int n_sub = (chunk_end - chunk_begin + S::ROWS - 1) / S::ROWS;
     float sum = 0.0f;
-    // passes and skips as the step
-    const bool part = part_launch(a.even_chunks, a.chunk, S::ROWS);
+    // passes and skips as the step (PART: the step's instance kind)
+    constexpr bool part = PART;
     const int sub0 = (part && n_sub > 1) ? chunk_id % n_sub : 0;
     for (int i = 0; i < n_sub; i++) {
         const int sub = sub0 + i < n_sub ? sub0 + i : sub0 + i - n_sub;

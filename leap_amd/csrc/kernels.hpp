@@ -24,7 +24,9 @@ constexpr int kThreads = kWaves * leap::kWave;
 // grid (measurement only).
 enum LaunchKind { kDecode = 0, kFloorLaunch = 1, kFloorStream = 2 };
 
-using KernelFn = void (*)(leap::StepArgs);
+// (the preloaded words, leap::Preload, then the argument block)
+using KernelFn = void (*)(const float *, const float *, float *, float *, const float4 *, uint32_t, uint32_t, uint32_t,
+                          uint32_t, leap::StepArgs);
 using MergeFn = void (*)(leap::StepArgs);
 
 // The decode kernel (or a floor kernel) for head_dim hd and g q heads per

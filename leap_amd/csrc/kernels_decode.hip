@@ -13,13 +13,17 @@ KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs)
         return nullptr;
     }
     if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8)) return nullptr;
-#define LEAP_CASE(HD, G)                                                                   \
-    if (hd == HD && g == G)                                                                \
-        return kind == kFloorLaunch ? leap::floor_launch_kernel<HD, G, kWaves>             \
-             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWaves> : nullptr;
+#define LEAP_STREAM(HD, G, K) \
+    (part ? leap::floor_stream_kernel<HD, G, kWaves, K, true> : leap::floor_stream_kernel<HD, G, kWaves, K, false>)
+#define LEAP_CASE(HD, G)                                                                             \
+    if (hd == HD && g == G)                                                                          \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>                     \
+             : kind == kFloorStream ? (kvs ? LEAP_STREAM(HD, G, true) : LEAP_STREAM(HD, G, false)) \
+                                      : nullptr;
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)
 #undef LEAP_CASE
+#undef LEAP_STREAM
     return nullptr;
 }
 

@@ -378,7 +378,7 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split != 0);
     if (!fn) return hipErrorInvalidValue;
     const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
-    if (n_chunk_max > s.max_chunks) return hipErrorInvalidValue;
+    if (n_chunk_max > s.max_chunks || s.n_kv_heads >= 65536) return hipErrorInvalidValue;  // (leap::Preload::w0)
     const long long n_groups = (long long)n_seq * s.n_kv_heads;
     int spread_log2 = 0;
     if (kind == kDecode && spreads(s, n_seq, total_rows))
@@ -439,7 +439,10 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     const int asym = (chunk <= 8 * leap::rows_per_pass(hd, s.group, kWaves) &&
                       n_pgroups * grid_x >= 2LL * launch_cus(s, n_seq, total_rows)) ? 1 : 0;
     a.merge_asym = asym | (s.fold_helper << 1);
-    hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, a);
+    // The prologue's words, preloaded into scalar registers (leap::Preload).
+    const leap::Preload p = leap::make_preload(a, n_seq == 1);
+    hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, p.q, p.k_new, p.k_cache, p.v_cache,
+                            p.rope, p.m_gc, p.w0, p.w1, p.w2, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
     MergeFn mf = pick_merge(hd, s.group);
     if (!mf) return hipErrorInvalidValue;
