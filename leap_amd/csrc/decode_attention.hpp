@@ -189,6 +189,27 @@ constexpr uint32_t kPreLimit = 1u << 21;  // pos, q < kPreLimit and n_chunks, r 
 constexpr unsigned kArgsOffset = 5 * sizeof(void *) + 4 * sizeof(uint32_t);
 static_assert(kArgsOffset == 56 && alignof(StepArgs) <= 8, "argument layout");
 
+// A kernel's argument block read at this point through a copy of the
+// kernel-argument pointer that the compiler cannot see through, so that none
+// of its loads (or a wait for one) is placed ahead of the loads before this
+// point; offset: the block's byte offset in the kernel arguments, after the
+// kernel's preloaded scalar arguments.
+template <class T>
+__device__ __forceinline__ T late_args(const T &host_side, unsigned offset)
+{
+#ifdef __HIP_DEVICE_COMPILE__
+    (void)host_side;
+    auto kargs = __builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kargs));
+    typedef __attribute__((address_space(4))) const T KernargT;
+    typedef __attribute__((address_space(4))) const char KernargBytes;
+    return *(KernargT *)((KernargBytes *)kargs + offset);
+#else
+    (void)offset;
+    return host_side;
+#endif
+}
+
 // The preloaded words of a launch (host side): the launch constants, and
 // the positions' words when it serves one sequence at host position pos
 // (one_seq), with chunk rows `chunk`, or even_chunks near-equal chunks.
@@ -779,19 +800,8 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
     __builtin_amdgcn_sched_barrier(0);
     load_v(sub0);
     __builtin_amdgcn_sched_barrier(0);
-    // The argument block, from here on: loaded through a copy of the
-    // kernel-argument pointer that the compiler cannot see through, so that
-    // none of its loads (or a wait for one) is placed ahead of the loads
-    // above.
-#ifdef __HIP_DEVICE_COMPILE__
-    auto kargs = __builtin_amdgcn_kernarg_segment_ptr();
-    asm volatile("" : "+s"(kargs));
-    typedef __attribute__((address_space(4))) const StepArgs KernargStepArgs;
-    typedef __attribute__((address_space(4))) const char KernargBytes;
-    const StepArgs a = *(KernargStepArgs *)((KernargBytes *)kargs + kArgsOffset);
-#else
-    const StepArgs &a = args;
-#endif
+    // The argument block, from here on (read after the loads above).
+    const StepArgs a = late_args(args, kArgsOffset);
     // every field the rest reads, as one batch of loads
     asm volatile("" ::"s"(a.v_new), "s"(a.scale_log2), "s"(a.out), "s"(a.ws_o), "s"(a.ws_ml), "s"(a.counters),
                  "s"(a.merge_asym), "s"(a.ws_po), "s"(a.ws_pml));

@@ -111,9 +111,16 @@ __device__ __forceinline__ float finish_dots(const gemv_f4 (&wv)[RB][NC], const 
 // (the reference's rsqrt estimate plus one Newton step rounds to within an
 // ulp or two of 1/sqrt).  Every workgroup normalises the (small) vector
 // itself while its weight rows are in flight, so no separate launch is needed.
+//
+// The kernels take their arguments as scalars, not as one struct: the
+// dispatch preloads the leading 14 argument words into scalar registers (the
+// library is built with -mllvm -amdgpu-kernarg-preload-count=14), so that
+// the first loads do not wait for a load of the arguments.
 template <int RB, int NC>
-__global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
+__global__ __launch_bounds__(kGemvThreads) void qkv_kernel(const float *x, const float *rms_w, const float *w,
+                                                           float *q, float *k, float *v, int dim, int kv_dim)
 {
+    const QkvArgs a{x, rms_w, w, q, k, v, dim, kv_dim};
     __shared__ float red[RB][kGemvWaves];
     __shared__ float ss_part[kGemvWaves];
     const int tid = threadIdx.x;
@@ -159,8 +166,9 @@ __global__ __launch_bounds__(kGemvThreads) void qkv_kernel(QkvArgs a)
 
 // x += W . xb
 template <int RB, int NC>
-__global__ __launch_bounds__(kGemvThreads) void proj_residual_kernel(ProjArgs a)
+__global__ __launch_bounds__(kGemvThreads) void proj_residual_kernel(const float *xb, const float *w, float *x, int d)
 {
+    const ProjArgs a{xb, w, x, d};
     __shared__ float red[RB][kGemvWaves];
     const int tid = threadIdx.x;
     const int n = NC * 4 * kGemvThreads;

@@ -174,9 +174,24 @@ constexpr int kQ8Waves = kQ8Threads / 64;
 // runtime row count the wait for the input had to assume the longest queue,
 // which made the normalisation wait for every weight row (0.8 us at
 // Llama-3-8B).  The input work now runs while the weights stream.
+//
+// Arguments: the input and weight pointers and the row count come first as
+// scalars, which the dispatch preloads into scalar registers (the library is
+// built with -mllvm -amdgpu-kernarg-preload-count=14), so that the first
+// loads do not wait for a load of the arguments; the rest of Q8Args (the
+// outputs) is read after the weight rows are issued (late_args).
+constexpr unsigned kQ8ArgsOffset = 4 * sizeof(void *) + 8;  // Q8Args after the preloaded x, rms_w, w, ws, rows
+static_assert(alignof(Q8Args) == 8, "argument layout");
+#define LEAP_Q8_PRELOAD_PARAMS const float *pre_x, const float *pre_rms_w, const int8_t *pre_w, const float *pre_ws, int pre_rows
 template <int E, int L, int RPT, int kIn, bool kResid, int ACT = kGemvThreads>
-__global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
+__global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(LEAP_Q8_PRELOAD_PARAMS, Q8Args args)
 {
+    Q8Args a{};
+    a.x = pre_x;
+    a.rms_w = pre_rms_w;
+    a.w = pre_w;
+    a.ws = pre_ws;
+    a.rows = pre_rows;
     constexpr int n = ACT * E;
     constexpr int NG = ACT / L;            // groups per row
     constexpr int VA = E / 4;              // input values per thread in the quantize step
@@ -316,6 +331,18 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
         }
     }
     __syncthreads();
+    // The outputs, from here on: the barriers above wait for every scalar
+    // load in flight, and these are needed only at the end.
+    {
+        const Q8Args late = late_args(args, kQ8ArgsOffset);
+        a.out0 = late.out0;
+        a.out1 = late.out1;
+        a.out2 = late.out2;
+        a.n0 = late.n0;
+        a.n1 = late.n1;
+        a.xq_out = late.xq_out;
+        a.xs_out = late.xs_out;
+    }
     if (blockIdx.x == 0 && a.xq_out) {  // the quantized input, for stage checks
         for (int i = tid; i < n / 4; i += kQ8Threads)
             reinterpret_cast<int *>(a.xq_out)[i] = reinterpret_cast<const int *>(lds_xq)[i];
@@ -380,8 +407,13 @@ __global__ __launch_bounds__(kQ8Threads) void q8_gemv_kernel(Q8Args a)
 // real data never meets.  The launch plus the bare weight stream of one
 // int8 projection.
 template <int E, int L, int RPT, int ACT = kGemvThreads>
-__global__ __launch_bounds__(kQ8Threads) void q8_floor_kernel(Q8Args a)
+__global__ __launch_bounds__(kQ8Threads) void q8_floor_kernel(LEAP_Q8_PRELOAD_PARAMS, Q8Args a)
 {
+    (void)pre_x;
+    (void)pre_rms_w;
+    a.w = pre_w;
+    a.ws = pre_ws;
+    a.rows = pre_rows;
     constexpr int n = ACT * E;
     constexpr int NG = ACT / L;
     constexpr int SLOTS = kQ8Teams * RPT;

@@ -49,14 +49,17 @@ extern template KernelFn pick_decode<128, true>(int, bool, bool);
 MergeFn pick_merge(int hd, int g);
 
 // The fp32 projections by dim = 1024 * NC: *rb rows per workgroup.
-using QkvFn = void (*)(leap::QkvArgs);
-using ProjFn = void (*)(leap::ProjArgs);
+// (the fields of leap::QkvArgs and leap::ProjArgs as scalar arguments, which
+// the dispatch preloads)
+using QkvFn = void (*)(const float *, const float *, const float *, float *, float *, float *, int, int);
+using ProjFn = void (*)(const float *, const float *, float *, int);
 // (w, rows, sink): the same grid streaming the weights alone (measurement)
 using GemvFloorFn = void (*)(const float *, int, float *);
 bool pick_proj(int dim, QkvFn *qkv, ProjFn *proj, int *rb, GemvFloorFn *floor = nullptr);
 
 // The int8 projections.
-using Q8Fn = void (*)(leap::Q8Args);
+// (x, rms_w, w, ws and rows preloaded, then leap::Q8Args)
+using Q8Fn = void (*)(const float *, const float *, const int8_t *, const float *, int, leap::Q8Args);
 // True if (dim, gs) has int8 kernels.
 bool q8_supported(int dim, int gs);
 // The kernel of `kind` (leap::kQ8InRms or leap::kQ8InF32) for `rows` rows:

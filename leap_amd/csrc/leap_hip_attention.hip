@@ -507,7 +507,8 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     Q8Fn fn = pick_q8(dim, gs, leap::kQ8InRms, (int)rows_qkv, h->n_cu, &rpt);
     if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     int per_wg = leap::kQ8Teams * rpt;
-    HIP_TRY(h, launch_k(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, qa));
+    HIP_TRY(h, launch_k(fn, dim3((unsigned)((rows_qkv + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, qa.x,
+                        qa.rms_w, qa.w, qa.ws, qa.rows, qa));
     int8_t *aq = h->q8_act + dim;
     float *as = h->q8_act_s + dim / gs;
     if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
@@ -523,7 +524,8 @@ int launch_block_q8(leap_hip_attention *h, int li, int layer, int pos, float *x,
     fn = pick_q8(dim, gs, leap::kQ8InF32, dim, h->n_cu, &rpt);
     if (!fn) return set_err(h, -EINVAL, "dim %d with group size %d has no int8 projection kernel", dim, gs);
     per_wg = leap::kQ8Teams * rpt;
-    HIP_TRY(h, launch_k(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, pa));
+    HIP_TRY(h, launch_k(fn, dim3((unsigned)((dim + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, pa.x,
+                        pa.rms_w, pa.w, pa.ws, pa.rows, pa));
     return 0;
 }
 
@@ -557,7 +559,8 @@ int launch_block_floor(leap_hip_attention *h, int layer, int pos, hipStream_t st
             qa.rows = rows;
             qa.out0 = sink;
             const int per_wg = leap::kQ8Teams * rpt;
-            HIP_TRY(h, launch_k(floor, dim3((unsigned)((rows + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream, qa));
+            HIP_TRY(h, launch_k(floor, dim3((unsigned)((rows + per_wg - 1) / per_wg)), dim3(leap::kQ8Threads), stream,
+                                qa.x, qa.rms_w, qa.w, qa.ws, qa.rows, qa));
         }
         return 0;
     }
@@ -599,14 +602,16 @@ int launch_block(leap_hip_attention *h, int layer, int pos, float *x, float *x_r
     qa.v = v;
     qa.dim = dim;
     qa.kv_dim = kv;
-    HIP_TRY(h, launch_k(qkv, dim3((unsigned)((dim + 2 * kv + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, qa));
+    HIP_TRY(h, launch_k(qkv, dim3((unsigned)((dim + 2 * kv + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, qa.x,
+                        qa.rms_w, qa.w, qa.q, qa.k, qa.v, qa.dim, qa.kv_dim));
     if (int rc = launch(h, layer, 1, nullptr, pos, pos, pos + 1, q, k, v, xb, stream)) return rc;
     leap::ProjArgs pa{};
     pa.xb = xb;
     pa.w = h->w_o + (size_t)li * dim * dim;
     pa.x = x_res;
     pa.d = dim;
-    HIP_TRY(h, launch_k(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, pa));
+    HIP_TRY(h, launch_k(proj, dim3((unsigned)((dim + rb - 1) / rb)), dim3(leap::kGemvThreads), stream, pa.xb, pa.w,
+                        pa.x, pa.d));
     return 0;
 }
 
