@@ -19,6 +19,14 @@ namespace leap_kernels {
 // Waves per workgroup of the decode kernel.
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * leap::kWave;
+// Waves per workgroup for chunks of at most half a kWaves pass (32 rows):
+// the short contexts' half-pass chunks and contexts of up to 32 positions,
+// which a 4-wave workgroup covers with two waves of masked rows.  Compiled
+// for the matrix-core products, with the PART instance kind, at head_dim 64
+// and at head_dim 128 with up to 4 q heads per KV head (the merge's layout
+// needs n_heads-of-the-group x head_dim / 4 threads at most, rounded up to
+// a power of two of heads).
+constexpr int kWavesShort = 2;
 
 // What a launch runs: the decode kernel, or one of the floor kernels with its
 // grid (measurement only).
@@ -34,16 +42,24 @@ using MergeFn = void (*)(leap::StepArgs);
 //   part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
 //         long (leap::part_launch);
 //   kvs:  two launch groups of g heads per cache head (kv_split; g = 8 only);
-//   valu: the score and weighted-V products as VALU FMAs (the A/B knob).
-KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs);
+//   valu: the score and weighted-V products as VALU FMAs (the A/B knob);
+//   waves: kWaves, or kWavesShort (part only, not valu or kvs;
+//          short_waves_shape).
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, int waves = kWaves);
+// Whether a shape has kWavesShort instances.
+constexpr bool short_waves_shape(int hd, int g)
+{
+    return (hd == 64 && (g == 1 || g == 2 || g == 3 || g == 4 || g == 8)) ||
+           (hd == 128 && (g == 1 || g == 2 || g == 3 || g == 4));
+}
 // The decode kernel alone, by head_dim HD and instance kind PART (one
 // translation unit per pair).
 template <int HD, bool PART>
-KernelFn pick_decode(int g, bool valu, bool kvs);
-extern template KernelFn pick_decode<64, false>(int, bool, bool);
-extern template KernelFn pick_decode<64, true>(int, bool, bool);
-extern template KernelFn pick_decode<128, false>(int, bool, bool);
-extern template KernelFn pick_decode<128, true>(int, bool, bool);
+KernelFn pick_decode(int g, bool valu, bool kvs, int waves);
+extern template KernelFn pick_decode<64, false>(int, bool, bool, int);
+extern template KernelFn pick_decode<64, true>(int, bool, bool, int);
+extern template KernelFn pick_decode<128, false>(int, bool, bool, int);
+extern template KernelFn pick_decode<128, true>(int, bool, bool, int);
 
 // The cross-XCD merge of a spread launch.
 MergeFn pick_merge(int hd, int g);

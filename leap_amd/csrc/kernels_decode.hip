@@ -5,14 +5,30 @@
 
 namespace leap_kernels {
 
-KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs)
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, int waves)
 {
     if (kind == kDecode) {
-        if (hd == 64) return part ? pick_decode<64, true>(g, valu, kvs) : pick_decode<64, false>(g, valu, kvs);
-        if (hd == 128) return part ? pick_decode<128, true>(g, valu, kvs) : pick_decode<128, false>(g, valu, kvs);
+        if (hd == 64)
+            return part ? pick_decode<64, true>(g, valu, kvs, waves) : pick_decode<64, false>(g, valu, kvs, waves);
+        if (hd == 128)
+            return part ? pick_decode<128, true>(g, valu, kvs, waves) : pick_decode<128, false>(g, valu, kvs, waves);
         return nullptr;
     }
     if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8)) return nullptr;
+    if (waves == kWavesShort) {
+        // the floors of the 2-wave launches: the same grid and block size
+        if (!part || kvs || !short_waves_shape(hd, g)) return nullptr;
+#define LEAP_CASE(HD, G)                                                                  \
+    if (hd == HD && g == G)                                                               \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWavesShort>      \
+             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWavesShort, false, true> \
+                                      : nullptr;
+        LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
+        LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4)
+#undef LEAP_CASE
+        return nullptr;
+    }
+    if (waves != kWaves) return nullptr;
 #define LEAP_STREAM(HD, G, K) \
     (part ? leap::floor_stream_kernel<HD, G, kWaves, K, true> : leap::floor_stream_kernel<HD, G, kWaves, K, false>)
 #define LEAP_CASE(HD, G)                                                                             \

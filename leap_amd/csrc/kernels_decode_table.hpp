@@ -7,8 +7,21 @@
 namespace leap_kernels {
 
 template <int HD, bool PART>
-KernelFn pick_decode(int g, bool valu, bool kvs)
+KernelFn pick_decode(int g, bool valu, bool kvs, int waves)
 {
+    if constexpr (PART) {
+        if (waves == kWavesShort) {
+            if (valu || kvs || !short_waves_shape(HD, g)) return nullptr;
+#define LEAP_CASE(G) \
+    if (g == G) return leap::decode_attention_kernel<HD, G, kWavesShort, true, true>;
+            LEAP_CASE(1) LEAP_CASE(2) LEAP_CASE(3) LEAP_CASE(4)
+#undef LEAP_CASE
+            if constexpr (HD == 64)
+                if (g == 8) return leap::decode_attention_kernel<64, 8, kWavesShort, true, true>;
+            return nullptr;
+        }
+    }
+    if (waves != kWaves) return nullptr;
 #define LEAP_CASE(G)                                                                                       \
     if (g == G && !kvs)                                                                                    \
         return valu ? leap::decode_attention_kernel<HD, G, kWaves, false, PART>                            \

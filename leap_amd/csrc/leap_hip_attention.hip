@@ -372,10 +372,24 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     const int hd = s.head_dim;
     const int even = even_chunks_for(s, n_seq, total_rows, max_pos + 1);
     const int chunk = even ? (max_pos + even) / even : choose_chunk(s, n_seq, total_rows, max_pos + 1);
+    // Chunks of at most half a pass (the short contexts' half-pass chunks,
+    // and contexts of up to 32 positions) run 2-wave workgroups, whose one
+    // pass is the chunk: a 4-wave workgroup gave them two waves of masked
+    // rows, whose empty loads and products still held up the combine.  Same
+    // process, graph replay, µs per layer-step: TinyLlama ctx 256 5.75 ->
+    // 5.34, ctx 130 5.48 -> 5.11, ctx 1 4.54 -> 4.33; Llama-3-8B heads ctx
+    // 256 5.71 -> 5.32, ctx 512 5.77 -> 5.44, ctx 1-32 4.00-4.17 ->
+    // 3.76-3.90.  Forced 32-row chunks at ctx 768-2048 stay slower than the
+    // automatic choice either way, so forced splits keep 4 waves.
+    const int waves = (short_waves_shape(hd, s.group) && !s.valu && s.kv_split == 0 && s.split == 0 && !even &&
+                       std::min(chunk, max_pos + 1) <= leap::rows_per_pass(hd, s.group, kWavesShort))
+                          ? kWavesShort
+                          : kWaves;
     // The PART instance: chunks that are not whole passes, and chunks of 2-8
-    // passes, whose pass order it rotates.
-    const bool part = leap::part_launch(even, chunk, leap::rows_per_pass(hd, s.group, kWaves));
-    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split != 0);
+    // passes, whose pass order it rotates (the 2-wave instances are all PART).
+    const bool part =
+        waves == kWavesShort || leap::part_launch(even, chunk, leap::rows_per_pass(hd, s.group, kWaves));
+    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split != 0, waves);
     if (!fn) return hipErrorInvalidValue;
     const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
     if (n_chunk_max > s.max_chunks || s.n_kv_heads >= 65536) return hipErrorInvalidValue;  // (leap::Preload::w0)
@@ -441,8 +455,8 @@ hipError_t launch_attention(const LaunchShape &s, const LaunchBuffers &b, int n_
     a.merge_asym = asym | (s.fold_helper << 1);
     // The prologue's words, preloaded into scalar registers (leap::Preload).
     const leap::Preload p = leap::make_preload(a, n_seq == 1);
-    hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3(kThreads), stream, p.q, p.k_new, p.k_cache, p.v_cache,
-                            p.rope, p.m_gc, p.w0, p.w1, p.w2, a);
+    hipError_t e = launch_k(fn, dim3((unsigned)n_wg), dim3((unsigned)(waves * leap::kWave)), stream, p.q, p.k_new,
+                            p.k_cache, p.v_cache, p.rope, p.m_gc, p.w0, p.w1, p.w2, a);
     if (e != hipSuccess || spread_log2 == 0) return e;
     MergeFn mf = pick_merge(hd, s.group);
     if (!mf) return hipErrorInvalidValue;

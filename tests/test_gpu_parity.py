@@ -96,8 +96,13 @@ SHAPES = [  # n_heads, n_kv_heads, head_dim
                                      # then of two passes
                                      (2500, 0), (3001, 0), (5000, 0),
                                      # automatic short contexts: half-pass chunks where a group has
-                                     # 2-8 one-pass chunks and the launch leaves CUs idle
-                                     (100, 0), (256, 0), (500, 0)])
+                                     # 2-8 one-pass chunks and the launch leaves CUs idle (2-wave
+                                     # workgroups where the shape has them)
+                                     (100, 0), (256, 0), (500, 0),
+                                     # up to 32 positions: one 2-wave workgroup per group where the
+                                     # shape has them; 33 takes a 4-wave one again; a forced 32-row
+                                     # split keeps 4 waves
+                                     (17, 0), (32, 0), (33, 0), (32, 32)])
 def test_step_shapes_and_splits(nh, nkv, hd, T, split):
     theta = 10000.0 if hd == 64 else 500000.0
     rng = rng_for(nh, nkv, hd, T, split)

@@ -113,6 +113,9 @@ def test_floor_launches_write_nothing(kind):
         att.floor_async(kind, 1, 3, 1000, 3 * 1001, s.cuda_stream)
         pos = torch.tensor([1000, 17, T - 1], dtype=torch.int32, device="cuda:0")
         att.floor_async(kind, 1, 3, T - 1, 1001 + 18 + T, s.cuda_stream, pos_ptr=pos.data_ptr())
+        # short contexts, whose steps run 2-wave workgroups (the floors too)
+        att.floor_async(kind, 1, 1, 20, 21, s.cuda_stream)
+        att.floor_async(kind, 1, 1, 255, 256, s.cuda_stream)
         s.synchronize()
         k1, v1 = att.kv_download(2, 1, 0, T)
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
