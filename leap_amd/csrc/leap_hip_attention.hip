@@ -297,11 +297,21 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         // merge (Llama-3-8B ctx 128 6.48 -> 6.11, 256 6.49 -> 6.16, 512 6.54
         // -> 6.27 us; 64 q heads at ctx 256 7.60 -> 7.21 us).  At 12 or more
         // chunks, or once the halved launch would fill more than half the
-        // CUs, they measured slower.
+        // CUs, they measured slower.  Shapes with 2-wave instances
+        // (launch_attention) run half-pass chunks without masked waves,
+        // which pays from up to 8 one-pass chunks and up to one half-pass
+        // workgroup per CU (graph replay: TinyLlama ctx 320 5.73 -> 5.52,
+        // 512 6.13 -> 5.64; 16/16/64 ctx 512 5.28 -> 4.72; 32 KV heads of
+        // one q head at ctx 256 5.82 -> 5.25; 16 of two at ctx 512 5.75 ->
+        // 5.27 us); two per CU made 32 KV heads at ctx 512 slower (6.46 ->
+        // 8.37 us), and 10-16 chunks stayed slower (Llama-3-8B heads ctx
+        // 640-1024 +0.4-0.5 us).
         const long long n_chunks = (max_T + quantum - 1) / quantum;
-        const bool few = n_chunks <= 4 || (n_chunks <= 8 && s.group <= 4 && s.head_dim == 128);
+        const bool two_waves = short_waves_shape(s.head_dim, s.group) && !s.valu && s.kv_split == 0;
+        const bool few = two_waves ? n_chunks <= 8
+                                   : n_chunks <= 4 || (n_chunks <= 8 && s.group <= 4 && s.head_dim == 128);
         if (bytes <= kLatencyBytes && !ragged && c == quantum && n_chunks >= 2 && few &&
-            4 * n_chunks * n_groups <= launch_cus(s, n_seq, total_rows))
+            (two_waves ? 2 : 4) * n_chunks * n_groups <= launch_cus(s, n_seq, total_rows))
             c = quantum / 2;
     }
     return std::max(c, std::max(floor_chunk, kSplitRows));
