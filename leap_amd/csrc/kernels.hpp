@@ -23,9 +23,9 @@ constexpr int kThreads = kWaves * leap::kWave;
 // the short contexts' half-pass chunks and contexts of up to 32 positions,
 // which a 4-wave workgroup covers with two waves of masked rows.  Compiled
 // for the matrix-core products, with the PART instance kind, at head_dim 64
-// and at head_dim 128 with up to 4 q heads per KV head (the merge's layout
-// needs n_heads-of-the-group x head_dim / 4 threads at most, rounded up to
-// a power of two of heads).
+// and at head_dim 128 with up to 4 q heads per KV head: the merge gives
+// each (head, float4 column) of the group at least one thread, and 128
+// threads cover 8 heads of 64 or 4 heads of 128.
 constexpr int kWavesShort = 2;
 
 // What a launch runs: the decode kernel, or one of the floor kernels with its
