@@ -580,12 +580,36 @@ __device__ __forceinline__ int fold_helper_wait(int *ctr, int target, int mode)
     return 0;
 }
 
+// The new token's cache rows, when the decode body leaves their stores to
+// the kernel's end: the rotated k and v_new of float4 column L in lane L.
+struct NewRow {
+    float4 k, v;
+    float *kdst, *vdst;
+    bool on;
+};
+
 template <int HD, int G, int NW, bool MFMA, bool PART, bool KVS>
-__device__ __forceinline__ void decode_attention_body(const StepArgs &args, const Preload &pre, Timeline &tl)
+__device__ __forceinline__ void decode_attention_body(const StepArgs &args, const Preload &pre, Timeline &tl,
+                                                      NewRow &nr)
 {
     using S = Shape<HD, G, NW>;
     constexpr int GQ = S::GQ, NF = S::NF, R = S::R, KS = S::KS;
     constexpr int LPV = S::LPV, RPV = S::RPV, VS = S::VS, D4 = S::D4, GM = S::GM, MG = S::MG;
+    // Where the new token's row (position pos) joins the scores and the
+    // weighted V.  Up to 4 q heads per KV head: after the loop, by the wave
+    // whose rows hold pos, with a score of its own (a dot product per head
+    // and a lane reduction); the loop masks row pos like the rows past it.
+    // Keeping the row out of the loop's products frees 60-100 registers of
+    // the loop (Llama-3-8B heads: 191 -> 120 VGPRs in the 4-wave partial-
+    // pass instance, 222 -> 123 in the whole-pass one, 190 -> 130 on 2
+    // waves), which measured faster with
+    // graph replay at every context of those heads: ctx 8192 15.50 -> 14.10
+    // us, 16384 25.59 -> 25.00, 2304 8.34 -> 8.16, 4096 9.63 -> 9.54.  With 8
+    // q heads the row stays in the loop's products (staged into the K and V
+    // registers of the row's load): added afterwards it measured slower for
+    // them (TinyLlama ctx 256 5.55 -> 6.18 us, Llama-3-405B ctx 4096 15.75 ->
+    // 17.06), eight heads of dependent reductions in one wave.
+    constexpr bool NEW_AFTER = G <= 4;
 
     // id = ((pg / 8) * grid_chunks + lc) * 8 + pg % 8, where the part-group
     // pg = group * 2^spread_log2 + part covers the group's chunks
@@ -674,18 +698,20 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
     // This chunk's rows [chunk_begin, last].  With PART a pass may reach past
     // the chunk's end.  Rows up to min(pos, chunk end) of this KV head are in
     // range: row pos (the new token, from registers) and the rows beyond
-    // read 0 without touching memory, and their scores are masked.
+    // read 0 without touching memory, and their scores are masked (row pos
+    // too when it is added after the loop).
+    constexpr int LAST_NEW = NEW_AFTER ? 1 : 0;
     int chunk_begin, chunk_end, row_end, last;
     if constexpr (PART) {
         chunk_begin = min(chunk_id * cq + min(chunk_id, cr), T);
         chunk_end = min((chunk_id + 1) * cq + min(chunk_id + 1, cr), T);
         row_end = min(pos, chunk_end);
-        last = min(pos, chunk_end - 1);
+        last = min(pos - LAST_NEW, chunk_end - 1);
     } else {
         chunk_begin = chunk_id * cq;
         chunk_end = min(chunk_begin + cq, T);
         row_end = pos;
-        last = pos;
+        last = pos - LAST_NEW;
     }
     const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(kc, (uint32_t)row_end * row_bytes);
     const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(vc, (uint32_t)row_end * row_bytes);
@@ -776,9 +802,10 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
     // empty outside the workgroup holding pos (those loads return 0 without
     // touching memory): without a branch, the waits (which count outstanding
     // loads in issue order) stay exact, and the prologue barrier waits for q
-    // alone.  The wave holding pos takes its lanes' parts of the k row
-    // through LDS, next to the table row (the q pairs' table entries), and
-    // of the v row across lanes.
+    // alone.  Added in the loop (8 q heads), the wave holding pos takes its
+    // lanes' parts of the k row through LDS, next to the table row (the q
+    // pairs' table entries), and of the v row across lanes; added after the
+    // loop, lane L < HD/4 rotates and scores float4 L of the row.
     const uint32_t new_bytes = has_pos ? (uint32_t)HD * 4u : 0u;
     const __amdgpu_buffer_rsrc_t kn_rsrc = make_rsrc(k_row_new, new_bytes);
     // (scheduling barriers keep the compiler from reordering the groups)
@@ -855,14 +882,15 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
             load_v(sub);
         }
 
-        // The new token's row: k_new, rotated exactly as the reference
-        // rotates it (it is stored), and v_new are appended to
+        // The new token's row, in the loop (8 q heads): k_new, rotated
+        // exactly as the reference rotates it (it is stored), and v_new are
+        // appended to
         // cache[layer][pos] and replace the (zero) loads of that row, k here
         // (the scores wait for the K loads anyway) and v just before the
         // weighted V (it is loaded last): overwriting a register whose load
         // is still in flight, or storing a loaded value, first waits for
         // that load.
-        const bool pos_here = (!PART || has_pos) && pos >= base && pos < base + R;  // wave-uniform
+        const bool pos_here = !NEW_AFTER && (!PART || has_pos) && pos >= base && pos < base + R;  // wave-uniform
         if (pos_here) {
             // k_new through the wave's staging: each lane reads its dims
             // 32*f + 4*ksl .. +3 of k_new and of the table row
@@ -1019,6 +1047,82 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
         __builtin_amdgcn_wave_barrier();
     }
     tl.mark(kTlLoopEnd);
+
+    // The new token's row after the loop (up to 4 q heads): the wave whose
+    // rows hold pos (its v_new load was issued after its rows' loads, and
+    // has arrived with them) rotates k_new in lanes L < HD/4 (float4 L, with
+    // float4 L of the table row that the prologue staged in this wave's
+    // combine buffer), scores it against each head (a dot product per lane,
+    // summed over the 16-lane rows with DPP and over the rows with
+    // v_readlane: wave-uniform), and adds p = 2^(s - m_ref) and p * v_new to
+    // the head's sum (lane 16's share of it, as score_rows_sum reads) and
+    // accumulators (lanes vg == 0: V row slot 0 of dims 4*vj .. +3), raising
+    // the reference max first if the score exceeds it by kLazyMax.  The
+    // heads' chains are independent and laid out step by step, so that they
+    // overlap.  The rotated k and v_new go to cache[layer][pos] when the
+    // kernel is done with everything else (NewRow), so that the merge's
+    // drain does not wait for them.
+    if constexpr (NEW_AFTER) {
+        if (has_pos && wave == ((pos - chunk_begin) % S::ROWS) / R) {
+            float4 krot = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (lane < D4) {
+                krot = rope4(knew_l, nt_lds[D4 + lane]);
+                if (store_new) {
+                    nr.k = krot;
+                    nr.v = vnew_l;
+                    nr.kdst = kc + (size_t)pos * kv_dim + 4 * lane;
+                    nr.vdst = vc + (size_t)pos * kv_dim + 4 * lane;
+                    nr.on = true;
+                }
+            }
+            float sh[G];
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float4 qv = q_lds[h][lane % D4];
+                const float d = qv.x * krot.x + qv.y * krot.y + qv.z * krot.z + qv.w * krot.w;
+                sh[h] = (lane < D4) ? d : 0.0f;
+            }
+#pragma unroll
+            for (int h = 0; h < G; h++) sh[h] += dpp<0x128>(sh[h]);  // row_ror:8
+#pragma unroll
+            for (int h = 0; h < G; h++) sh[h] += dpp<0x124>(sh[h]);  // row_ror:4
+#pragma unroll
+            for (int h = 0; h < G; h++) sh[h] += dpp<0x122>(sh[h]);  // row_ror:2
+#pragma unroll
+            for (int h = 0; h < G; h++) sh[h] += dpp<0x121>(sh[h]);  // row_ror:1
+            bool grow = false;
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                // the rows that hold dims: one at head_dim 64, two at 128
+                float v = lane_value(sh[h], 0);
+#pragma unroll
+                for (int row = 1; row < D4 / 16; row++) v += lane_value(sh[h], 16 * row);
+                sh[h] = v;
+                grow |= sh[h] > m_ref[h] + kLazyMax;
+            }
+            if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+                for (int h = 0; h < G; h++) {
+                    const float m_new = fmaxf(m_ref[h], sh[h]);
+                    const float alpha = (m_ref[h] == -INFINITY) ? 0.0f : fast_exp2(m_ref[h] - m_new);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[h / 4][e][h % 4] *= alpha;
+                    l_run[h] *= alpha;
+                    m_ref[h] = m_new;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float p = fast_exp2(sh[h] - m_ref[h]);
+                l_run[h] += (lane == 16) ? p : 0.0f;
+                const float pv = (vg == 0) ? p : 0.0f;
+                acc[h / 4][0][h % 4] += pv * vnew_l.x;
+                acc[h / 4][1][h % 4] += pv * vnew_l.y;
+                acc[h / 4][2][h % 4] += pv * vnew_l.z;
+                acc[h / 4][3][h % 4] += pv * vnew_l.w;
+            }
+        }
+    }
 
     // Per-wave partials to LDS: every V row slot its own accumulator.
 #pragma unroll
@@ -1485,7 +1589,13 @@ __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) 
 {
     Timeline tl;
     tl.mark(kTlStart);
-    decode_attention_body<HD, G, NW, MFMA, PART, KVS>(a, LEAP_PRELOAD, tl);
+    NewRow nr;
+    nr.on = false;
+    decode_attention_body<HD, G, NW, MFMA, PART, KVS>(a, LEAP_PRELOAD, tl, nr);
+    if (nr.on) {
+        *reinterpret_cast<float4 *>(nr.kdst) = nr.k;
+        *reinterpret_cast<float4 *>(nr.vdst) = nr.v;
+    }
 #ifdef LEAP_TIMELINE
     tl.mark(kTlEnd);
     tl.flush(a.tl);
