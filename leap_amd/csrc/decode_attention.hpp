@@ -880,6 +880,14 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
         if (i > 0) {
             load_k(sub);
             load_v(sub);
+            // Every load of the pass goes out before its products.  Below
+            // 128 VGPRs the compiler's scheduler, aiming at more waves per
+            // SIMD, moved each load next to its first use, into the register
+            // that the previous product had just freed, which put a memory
+            // round trip between products of one pass: Llama-3.1-8B ctx
+            // 131072 (one workgroup per CU, 64 passes per chunk) 157 -> 188
+            // us per launch.
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         // The new token's row, in the loop (8 q heads): k_new, rotated
