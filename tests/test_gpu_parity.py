@@ -138,6 +138,34 @@ def test_valu_products_shapes_and_splits(nh, nkv, hd, T, split):
         _step_and_check(att, 0, pos, q, k, v, theta, out=out)
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (32, 4, 64), (24, 8, 128), (8, 8, 128), (16, 8, 64),
+                                       (64, 8, 128)])
+@pytest.mark.parametrize("T", [1, 2, 33, 65, 257, 2080, 4096])
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_new_token_score_dominates_or_vanishes(nh, nkv, hd, T, sign):
+    """The q heads of a group close to one direction u (u + 0.05 noise) and
+    k_new = +-2000 u: the new token's score exceeds every cached score by far
+    more than the lazy max's margin (the running max is raised for it, and
+    the output is about v_new), or its weight underflows to zero.  RoPE
+    rotates q and k by the same angles, so the score keeps its size."""
+    theta = 10000.0 if hd == 64 else 500000.0
+    rng = rng_for(nh, nkv, hd, T, int(sign > 0))
+    g = nh // nkv
+    with HipAttention(nh, nkv, hd, T + 3, rope_theta=theta) as att:
+        pos = T - 1
+        if pos:
+            att.kv_upload(0, 0, 0, normal(rng, (pos, nkv * hd), hd), normal(rng, (pos, nkv * hd), hd))
+        u = normal(rng, (nkv, 1, hd), hd)
+        q = (u + 0.05 * normal(rng, (nkv, g, hd), hd)).astype(np.float32).reshape(-1)
+        k = (sign * 2000.0 * u).astype(np.float32).reshape(-1)
+        v = normal(rng, nkv * hd, hd)
+        out = att.step(0, pos, q, k, v)
+        _step_and_check(att, 0, pos, q, k, v, theta, out=out)
+        if sign > 0:  # every head of a group takes (nearly) its group's v_new
+            want = np.repeat(v.reshape(nkv, 1, hd), g, axis=1).reshape(-1)
+            assert_close(out, want, rel=1e-3, what="dominant new token")
+
+
 def test_first_position_returns_v_exactly():
     with HipAttention(32, 8, 128, 16) as att:
         rng = rng_for(5)
