@@ -42,10 +42,10 @@ using MergeFn = void (*)(leap::StepArgs);
 //   part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
 //         long (leap::part_launch);
 //   kvs:  two launch groups of g heads per cache head (kv_split): g = 8 for
-//         16 q heads per KV head, g = 4 (MFMA products) for 8;
+//         16 q heads per KV head, g = 4 and 2 (MFMA products) for 8 and 4;
 //   valu: the score and weighted-V products as VALU FMAs (the A/B knob);
-//   waves: kWaves, or kWavesShort (part only, not valu, kvs with g = 4
-//          only; short_waves_shape).
+//   waves: kWaves, or kWavesShort (part only, not valu, kvs with g = 2 and
+//          4 only; short_waves_shape).
 KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, int waves = kWaves);
 // Whether a shape has kWavesShort instances.
 constexpr bool short_waves_shape(int hd, int g)

@@ -14,19 +14,19 @@ KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, in
             return part ? pick_decode<128, true>(g, valu, kvs, waves) : pick_decode<128, false>(g, valu, kvs, waves);
         return nullptr;
     }
-    if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8 && g != 4)) return nullptr;
+    if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8 && g != 4 && g != 2)) return nullptr;
     if (waves == kWavesShort) {
         // the floors of the 2-wave launches: the same grid and block size
         if (!part || !short_waves_shape(hd, g)) return nullptr;
-        if (kvs) {  // two launch groups of 4 q heads per cache head
-            if (g != 4) return nullptr;
-            if (hd == 64)
-                return kind == kFloorLaunch   ? leap::floor_launch_kernel<64, 4, kWavesShort>
-                     : kind == kFloorStream ? leap::floor_stream_kernel<64, 4, kWavesShort, true, true>
-                                              : nullptr;
-            return kind == kFloorLaunch   ? leap::floor_launch_kernel<128, 4, kWavesShort>
-                 : kind == kFloorStream ? leap::floor_stream_kernel<128, 4, kWavesShort, true, true>
-                                          : nullptr;
+        if (kvs) {  // two launch groups of 2 or 4 q heads per cache head
+#define LEAP_KVS_CASE(HD, G)                                                              \
+    if (hd == HD && g == G)                                                               \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWavesShort>      \
+             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWavesShort, true, true> \
+                                      : nullptr;
+            LEAP_KVS_CASE(64, 2) LEAP_KVS_CASE(64, 4) LEAP_KVS_CASE(128, 2) LEAP_KVS_CASE(128, 4)
+#undef LEAP_KVS_CASE
+            return nullptr;
         }
 #define LEAP_CASE(HD, G)                                                                  \
     if (hd == HD && g == G)                                                               \

@@ -197,32 +197,37 @@ LaunchShape shape_of(const leap_hip_attention *h)
     return s;
 }
 
-// Launches of 8 q heads per KV head that move at most kTwinBytes of K/V
-// rows, over at most kXcds (sequence, KV head) groups, run as two launch
-// groups of 4 q heads per cache head (kv_split, instances of their own):
-// each workgroup reads its chunk's rows for half the heads, so the launch
-// has twice the workgroups, each with half the score, softmax, combine and
-// fold work.  Same process, both orders, graph replay, µs per layer-step:
-// TinyLlama ctx 1 4.33 -> 3.62, 256 5.51 -> 4.95, 1024 6.14 -> 5.53, 4096
-// 8.41 -> 7.75, 8192 11.73 -> 10.50; the 70B heads ctx 512 7.11 -> 5.57,
-// 1024 7.43 -> 6.19, 2048 8.84 -> 8.40, 3072 10.50 -> 10.38; 4 KV heads of
-// 8 at head_dim 128 ctx 4096 11.27 -> 9.57; one KV head ctx 4096 11.61 ->
-// 8.85.  Reading every row twice loses once the launch streams: the 70B
-// heads at ctx 4096 (32 MiB) 11.67 -> 12.30, TinyLlama at 32768 23.1 ->
-// 26.1, one KV head at 32768 16.8 -> 18.3.
-constexpr long long kTwinBytes = 24ll << 20;
+// Small launches of 4 or 8 q heads per KV head, over at most kXcds
+// (sequence, KV head) groups, run as two launch groups of 2 or 4 q heads per
+// cache head (kv_split, instances of their own): each workgroup reads its
+// chunk's rows for half the heads, so the launch has twice the workgroups,
+// each with half the score, softmax, combine and fold work.  Same process,
+// both orders, graph replay, µs per layer-step, 8 q heads per KV head (up to
+// 24 MiB of K/V rows): TinyLlama ctx 1 4.33 -> 3.62, 256 5.51 -> 4.95, 1024
+// 6.14 -> 5.53, 4096 8.41 -> 7.75, 8192 11.73 -> 10.50; the 70B heads ctx
+// 512 7.11 -> 5.57, 1024 7.43 -> 6.19, 2048 8.84 -> 8.40, 3072 10.50 ->
+// 10.38; 4 KV heads of 8 at head_dim 128 ctx 4096 11.27 -> 9.57; one KV head
+// ctx 4096 11.61 -> 8.85.  4 q heads per KV head (up to 8 MiB): Llama-3-8B
+// heads ctx 1 3.82 -> 3.51, 256 5.32-5.38 -> 4.95, 512 5.46 -> 5.11, 1024
+// 6.05 -> 5.83.  Reading every row twice loses once the launch streams: the
+// 70B heads at ctx 4096 (32 MiB) 11.67 -> 12.30, TinyLlama at 32768 23.1 ->
+// 26.1, one KV head at 32768 16.8 -> 18.3, Llama-3-8B heads at ctx 2048 (16
+// MiB) 6.81 -> 8.09.
+long long twin_bytes(int group)
+{
+    return group == 8 ? 24ll << 20 : group == 4 ? 8ll << 20 : -1;
+}
 LaunchShape launch_view(const LaunchShape &s, int n_seq, long long total_rows)
 {
     LaunchShape v = s;
-    if (s.group == 8 && s.kv_split == 0 && !s.valu && (long long)n_seq * s.n_kv_heads <= leap::kXcds &&
-        total_rows * s.n_kv_heads * s.head_dim * 8ll <= kTwinBytes) {
-        v.group = 4;
+    if (s.kv_split == 0 && !s.valu && (long long)n_seq * s.n_kv_heads <= leap::kXcds &&
+        total_rows * s.n_kv_heads * s.head_dim * 8ll <= twin_bytes(s.group)) {
+        v.group = s.group / 2;
         v.n_kv_heads = 2 * s.n_kv_heads;
         v.kv_split = 1;
     }
     return v;
 }
-
 
 // Positions per workgroup (chunk), from the size and shape of the launch:
 //   - small launches (K/V bytes up to kLatencyBytes) are latency-bound: two
@@ -334,7 +339,7 @@ int choose_chunk(const LaunchShape &s, int n_seq, long long total_rows, int max_
         // 8.37 us), and 10-16 chunks stayed slower (Llama-3-8B heads ctx
         // 640-1024 +0.4-0.5 us).
         const long long n_chunks = (max_T + quantum - 1) / quantum;
-        const bool two_waves = short_waves_shape(s.head_dim, s.group) && !s.valu && (s.kv_split == 0 || s.group == 4);
+        const bool two_waves = short_waves_shape(s.head_dim, s.group) && !s.valu && (s.kv_split == 0 || s.group <= 4);
         const bool few = two_waves ? n_chunks <= 8
                                    : n_chunks <= 4 || (n_chunks <= 8 && s.group <= 4 && s.head_dim == 128);
         if (bytes <= kLatencyBytes && !ragged && c == quantum && n_chunks >= 2 && few &&
@@ -419,7 +424,7 @@ hipError_t launch_attention(const LaunchShape &shape, const LaunchBuffers &b, in
     // 256 5.71 -> 5.32, ctx 512 5.77 -> 5.44, ctx 1-32 4.00-4.17 ->
     // 3.76-3.90.  Forced 32-row chunks at ctx 768-2048 stay slower than the
     // automatic choice either way, so forced splits keep 4 waves.
-    const int waves = (short_waves_shape(hd, s.group) && !s.valu && (s.kv_split == 0 || s.group == 4) &&
+    const int waves = (short_waves_shape(hd, s.group) && !s.valu && (s.kv_split == 0 || s.group <= 4) &&
                        s.split == 0 && !even &&
                        std::min(chunk, max_pos + 1) <= leap::rows_per_pass(hd, s.group, kWavesShort))
                           ? kWavesShort
@@ -835,9 +840,9 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     const size_t ws_rows = n_pg * kvv.group * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    // (launch_view's two groups of 4 q heads per cache head: up to 2 kXcds
-    // groups, whose records fit in those of kXcds groups of 8)
-    const bool twins = kvv.group == 8 && kvv.kv_split == 0;
+    // (launch_view's two groups of 2 or 4 q heads per cache head: up to 2
+    // kXcds groups, whose records fit in those of kXcds groups of 4 or 8)
+    const bool twins = (kvv.group == 8 || kvv.group == 4) && kvv.kv_split == 0;
     const size_t n_ctr = std::max<size_t>(n_pg, twins ? 2 * leap::kXcds : 0);
     h->counter_bytes = n_ctr * leap::counters_per_group(h->max_chunks) * sizeof(int);
     CREATE_TRY(hipMalloc(&h->ws_po, (size_t)leap::kXcds * h->group * c.head_dim * sizeof(float)));

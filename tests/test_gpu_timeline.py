@@ -27,8 +27,8 @@ def _ring(lib):
 
 @pytest.mark.parametrize("nh,nkv,hd,T,n_wg", [
     (32, 8, 128, 4096, 512),  # 64 one-pass chunks per KV head: the asymmetric merge with the fold helper
-    (32, 8, 128, 1000, 128),  # 16 chunks per KV head: the one-level merge
-    (16, 4, 64, 50, 8),       # one chunk per KV head: the output written directly (4 of 8 workgroups idle)
+    (24, 8, 128, 1000, 128),  # 16 chunks per KV head: the one-level merge
+    (8, 4, 64, 50, 8),        # one chunk per KV head: the output written directly (4 of 8 workgroups idle)
     (32, 4, 64, 50, 8),       # 8 q heads per KV head: two launch groups of 4 per cache head, none idle
 ])
 def test_timeline_build_matches_and_stamps_in_order(hip_device, nh, nkv, hd, T, n_wg):
@@ -58,8 +58,10 @@ def test_timeline_build_matches_and_stamps_in_order(hip_device, nh, nkv, hd, T, 
     t = ring[(launches - 1) % SLOTS, :n_wg]
     assert (t[:, START] > 0).all() and (t[:, END] >= t[:, START]).all()
     assert (ring[(launches - 1) % SLOTS, n_wg:, START] == 0).all()  # no workgroup beyond the grid
-    # launch groups: a launch this small runs 8 q heads per KV head as two groups of 4
-    groups = 2 * nkv if nh // nkv == 8 else nkv
+    # launch groups: small launches run 4 or 8 q heads per KV head as two
+    # groups of 2 or 4 per cache head (up to 8 and 24 MiB of K/V rows)
+    limit = {4: 8 << 20, 8: 24 << 20}.get(nh // nkv, -1)
+    groups = 2 * nkv if T * nkv * hd * 8 <= limit else nkv
     # workgroup ids equal modulo 8 are one KV head's chunks; ids of the
     # missing heads (fewer than 8) leave at once
     idle = (np.arange(n_wg) % 8) >= groups
