@@ -296,6 +296,35 @@ def test_batched_small_ragged_with_tiny_contexts(split):
             _step_and_check(att, 0, int(Ts[i]) - 1, q[i], k[i], v[i], 500000.0, seq=i, out=out[i])
 
 
+@pytest.mark.parametrize("nh,nkv,hd,Ts", [
+    # 8 q heads per KV head: two launch groups of 4 per cache head up to 24 MiB
+    # of K/V rows (TinyLlama: 12288 positions) over at most 8 groups
+    (32, 4, 64, [12288]), (32, 4, 64, [12289]),
+    (64, 8, 128, [3072]), (64, 8, 128, [3073]),
+    (8, 1, 128, [24576]), (8, 1, 128, [24577]),        # one KV head: spread over the XCDs either way
+    # 4 q heads per KV head: groups of 2 up to 8 MiB (Llama-3-8B heads: 1024)
+    (32, 8, 128, [1024]), (32, 8, 128, [1025]), (16, 4, 64, [4096]), (16, 4, 64, [4097]),
+    # batches: up to 8 (sequence, KV head) groups
+    (32, 4, 64, [700, 33]), (32, 4, 64, [700, 33, 1]), (32, 8, 128, [40]), (32, 8, 128, [40, 40]),
+    (16, 2, 128, [3000, 17, 2, 1]), (16, 2, 128, [3000, 17, 2, 1, 64]),
+])
+def test_twin_launch_group_limits(nh, nkv, hd, Ts):
+    """Launches on either side of the twin launch groups' limits (K/V bytes,
+    groups per launch), single and batched, against the oracle."""
+    theta = 10000.0 if hd == 64 else 500000.0
+    Ts = np.array(Ts)
+    S = len(Ts)
+    rng = rng_for(nh, nkv, hd, int(Ts.sum()), S)
+    with HipAttention(nh, nkv, hd, int(Ts.max()) + 1, rope_theta=theta, max_batch=max(S, 1)) as att:
+        att.kv_fill_normal(0x7417 + S, 1.0 / np.sqrt(hd))
+        q = normal(rng, (S, nh * hd), hd)
+        k = normal(rng, (S, nkv * hd), hd)
+        v = normal(rng, (S, nkv * hd), hd)
+        out = att.step_batched(0, Ts - 1, q, k, v)
+        for i in range(S):
+            _step_and_check(att, 0, int(Ts[i]) - 1, q[i], k[i], v[i], theta, seq=i, out=out[i])
+
+
 @pytest.mark.parametrize("nh,nkv,hd,Ts,split", [
     # at least two groups per XCD take one workgroup per CU:
     (32, 8, 128, [1500, 1100], 0),       # 16 groups: 16 near-equal chunks each
