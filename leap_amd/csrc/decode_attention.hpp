@@ -297,20 +297,21 @@ struct Timeline {
 };
 
 // The cache's KV head and the first q head of a launch's KV group kvv (of
-// n_kv_heads).  With kv_split, the cache holds n_kv = n_kv_heads / 2 heads of
-// 2G q heads each, served as two groups of G: half 0 is groups [0, n_kv),
-// half 1 groups [n_kv, 2 n_kv), so that with n_kv a multiple of 8 both halves
-// of a head run on one XCD and the second read of its rows can hit in L2.
+// n_kv_heads).  With kv_split = k (1 or 2), the cache holds n_kv =
+// n_kv_heads >> k heads of 2^k G q heads each, served as 2^k groups of G:
+// part p is groups [p n_kv, (p + 1) n_kv), so that with n_kv a multiple of 8
+// every part of a head runs on one XCD and the later reads of its rows can
+// hit in L2.
 struct KvGroup {
-    int kvh, half, qh0;
+    int kvh, half, qh0;  // half: the part (0 appends the new token)
 };
 template <int G>
 __device__ __forceinline__ KvGroup kv_group(int kvv, int n_kv_heads, int kv_split)
 {
     const int n_kv = n_kv_heads >> kv_split;
-    const int half = kvv >= n_kv ? 1 : 0;
-    const int kvh = kvv - half * n_kv;
-    return KvGroup{kvh, half, ((kvh << kv_split) + half) * G};
+    const int part = (kvv >= n_kv ? 1 : 0) + (kvv >= 2 * n_kv ? 1 : 0) + (kvv >= 3 * n_kv ? 1 : 0);
+    const int kvh = kvv - part * n_kv;
+    return KvGroup{kvh, part, ((kvh << kv_split) + part) * G};
 }
 
 // Whether a launch runs the PART instance of the decode kernel (the host's
@@ -588,7 +589,7 @@ struct NewRow {
     bool on;
 };
 
-template <int HD, int G, int NW, bool MFMA, bool PART, bool KVS>
+template <int HD, int G, int NW, bool MFMA, bool PART, int KVS>
 __device__ __forceinline__ void decode_attention_body(const StepArgs &args, const Preload &pre, Timeline &tl,
                                                       NewRow &nr)
 {
@@ -657,7 +658,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
             // skip is visible (the first chunk of each group writes its
             // heads; a spread launch's merge launch does it instead).
             const int kvv = group - seq * n_kv_heads;
-            const int qh0 = KVS ? kv_group<G>(kvv, n_kv_heads, 1).qh0 : kvv * G;
+            const int qh0 = KVS ? kv_group<G>(kvv, n_kv_heads, KVS).qh0 : kvv * G;
             if (chunk_id == 0 && spread_log2 == 0)
                 for (int i = threadIdx.x; i < G * HD; i += NW * kWave)
                     args.out[(size_t)seq * args.n_heads * HD + (size_t)qh0 * HD + i] = __builtin_nanf("");
@@ -676,9 +677,9 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
         slab = (size_t)seq * (size_t)args.seq_stride;
     }
     const int kvv = group - seq * n_kv_heads;  // the group within its sequence
-    // KVS: two launch groups per cache head (kv_split set), compiled as
+    // KVS: 2^KVS launch groups per cache head (kv_split = KVS), compiled as
     // instances of their own so that the others keep their code
-    const KvGroup kg = KVS ? kv_group<G>(kvv, n_kv_heads, 1) : KvGroup{kvv, 0, kvv * G};
+    const KvGroup kg = KVS ? kv_group<G>(kvv, n_kv_heads, KVS) : KvGroup{kvv, 0, kvv * G};
     const int kvh = kg.kvh;
     const bool store_new = kg.half == 0;  // the one group per cache head that appends the new token
     const int tid = threadIdx.x;
@@ -690,7 +691,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
     // chunks of this part (at least 1 here)
     const int n_local = min(grid_chunks, n_chunks - part * grid_chunks);
 
-    const int kv_dim = (KVS ? n_kv_heads / 2 : n_kv_heads) * HD;
+    const int kv_dim = (n_kv_heads >> KVS) * HD;
     const int q_dim = n_kv_heads * G * HD;  // every q head of a sequence
     const uint32_t row_bytes = (uint32_t)kv_dim * 4u;
     float *kc = pre.k_cache + slab + (size_t)kvh * HD;
@@ -1592,7 +1593,7 @@ __device__ __forceinline__ void decode_attention_body(const StepArgs &args, cons
     tl.mark(kTlFolded);
 }
 
-template <int HD, int G, int NW, bool MFMA = true, bool PART = false, bool KVS = false>
+template <int HD, int G, int NW, bool MFMA = true, bool PART = false, int KVS = 0>
 __global__ __launch_bounds__(NW * kWave, (MFMA && G == 8 && HD == 128) ? 2 : 1) void decode_attention_kernel(LEAP_PRELOAD_PARAMS, StepArgs a)
 {
     Timeline tl;
@@ -1672,7 +1673,7 @@ __global__ __launch_bounds__(NW * kWave) void floor_launch_kernel(LEAP_PRELOAD_P
     if (pre_w0 == 0u && pre_w1 == 0u) a.out[threadIdx.x] = 0.0f;
 }
 
-template <int HD, int G, int NW, bool KVS, bool PART>
+template <int HD, int G, int NW, int KVS, bool PART>
 __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(LEAP_PRELOAD_PARAMS, StepArgs a)
 {
     using S = Shape<HD, G, NW>;
@@ -1715,11 +1716,11 @@ __global__ __launch_bounds__(NW * kWave) void floor_stream_kernel(LEAP_PRELOAD_P
         }
         slab = (size_t)seq * (size_t)a.seq_stride;
     }
-    const int kvh = kv_group<G>(group - seq * n_kv_heads, n_kv_heads, KVS ? 1 : 0).kvh;
+    const int kvh = kv_group<G>(group - seq * n_kv_heads, n_kv_heads, KVS).kvh;
     const int T = pos + 1;
     if (chunk_id >= n_chunks) return;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const uint32_t row_bytes = (uint32_t)((KVS ? n_kv_heads / 2 : n_kv_heads) * HD) * 4u;
+    const uint32_t row_bytes = (uint32_t)((n_kv_heads >> KVS) * HD) * 4u;
     const int chunk_begin = min(chunk_id * cq + min(chunk_id, cr), T);
     const int chunk_end = min((chunk_id + 1) * cq + min(chunk_id + 1, cr), T);
     const uint32_t range = (uint32_t)min(pos, chunk_end) * row_bytes;  // as the step's

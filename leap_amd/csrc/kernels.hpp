@@ -41,12 +41,13 @@ using MergeFn = void (*)(leap::StepArgs);
 // launch group; nullptr for a shape without one.
 //   part: the launch's chunks are near-equal, not whole passes, or 2-8 passes
 //         long (leap::part_launch);
-//   kvs:  two launch groups of g heads per cache head (kv_split): g = 8 for
-//         16 q heads per KV head, g = 4 and 2 (MFMA products) for 8 and 4;
+//   kvs:  the launch's kv_split k: 2^k launch groups of g heads per cache
+//         head (0: one); k = 1 with g = 8 for 16 q heads per KV head, g = 4
+//         and 2 (MFMA products) for 8 and 4; k = 2 with g = 2 for 8;
 //   valu: the score and weighted-V products as VALU FMAs (the A/B knob);
-//   waves: kWaves, or kWavesShort (part only, not valu, kvs with g = 2 and
-//          4 only; short_waves_shape).
-KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, int waves = kWaves);
+//   waves: kWaves, or kWavesShort (part only, not valu, with kvs only at
+//          g = 2 and 4; short_waves_shape).
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, int kvs, int waves = kWaves);
 // Whether a shape has kWavesShort instances.
 constexpr bool short_waves_shape(int hd, int g)
 {
@@ -56,11 +57,11 @@ constexpr bool short_waves_shape(int hd, int g)
 // The decode kernel alone, by head_dim HD and instance kind PART (one
 // translation unit per pair).
 template <int HD, bool PART>
-KernelFn pick_decode(int g, bool valu, bool kvs, int waves);
-extern template KernelFn pick_decode<64, false>(int, bool, bool, int);
-extern template KernelFn pick_decode<64, true>(int, bool, bool, int);
-extern template KernelFn pick_decode<128, false>(int, bool, bool, int);
-extern template KernelFn pick_decode<128, true>(int, bool, bool, int);
+KernelFn pick_decode(int g, bool valu, int kvs, int waves);
+extern template KernelFn pick_decode<64, false>(int, bool, int, int);
+extern template KernelFn pick_decode<64, true>(int, bool, int, int);
+extern template KernelFn pick_decode<128, false>(int, bool, int, int);
+extern template KernelFn pick_decode<128, true>(int, bool, int, int);
 
 // The cross-XCD merge of a spread launch.
 MergeFn pick_merge(int hd, int g);

@@ -5,7 +5,7 @@
 
 namespace leap_kernels {
 
-KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, int waves)
+KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, int kvs, int waves)
 {
     if (kind == kDecode) {
         if (hd == 64)
@@ -14,17 +14,20 @@ KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, in
             return part ? pick_decode<128, true>(g, valu, kvs, waves) : pick_decode<128, false>(g, valu, kvs, waves);
         return nullptr;
     }
-    if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || (kvs && g != 8 && g != 4 && g != 2)) return nullptr;
+    if ((g != 1 && g != 2 && g != 3 && g != 4 && g != 8) || kvs < 0 || kvs > 2 || (kvs == 1 && g != 8 && g != 4 && g != 2) ||
+        (kvs == 2 && g != 2))
+        return nullptr;
     if (waves == kWavesShort) {
         // the floors of the 2-wave launches: the same grid and block size
         if (!part || !short_waves_shape(hd, g)) return nullptr;
-        if (kvs) {  // two launch groups of 2 or 4 q heads per cache head
-#define LEAP_KVS_CASE(HD, G)                                                              \
-    if (hd == HD && g == G)                                                               \
-        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWavesShort>      \
-             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWavesShort, true, true> \
+        if (kvs) {  // two launch groups of 2 or 4 q heads per cache head, or four of 2
+#define LEAP_KVS_CASE(HD, G, K)                                                              \
+    if (hd == HD && g == G && kvs == K)                                                      \
+        return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWavesShort>         \
+             : kind == kFloorStream ? leap::floor_stream_kernel<HD, G, kWavesShort, K, true> \
                                       : nullptr;
-            LEAP_KVS_CASE(64, 2) LEAP_KVS_CASE(64, 4) LEAP_KVS_CASE(128, 2) LEAP_KVS_CASE(128, 4)
+            LEAP_KVS_CASE(64, 2, 1) LEAP_KVS_CASE(64, 4, 1) LEAP_KVS_CASE(128, 2, 1) LEAP_KVS_CASE(128, 4, 1)
+            LEAP_KVS_CASE(64, 2, 2) LEAP_KVS_CASE(128, 2, 2)
 #undef LEAP_KVS_CASE
             return nullptr;
         }
@@ -44,7 +47,7 @@ KernelFn pick_kernel(int hd, int g, int kind, bool valu, bool part, bool kvs, in
 #define LEAP_CASE(HD, G)                                                                             \
     if (hd == HD && g == G)                                                                          \
         return kind == kFloorLaunch   ? leap::floor_launch_kernel<HD, G, kWaves>                     \
-             : kind == kFloorStream ? (kvs ? LEAP_STREAM(HD, G, true) : LEAP_STREAM(HD, G, false)) \
+             : kind == kFloorStream ? (kvs == 2 ? LEAP_STREAM(HD, G, 2) : kvs ? LEAP_STREAM(HD, G, 1) : LEAP_STREAM(HD, G, 0)) \
                                       : nullptr;
     LEAP_CASE(64, 1) LEAP_CASE(64, 2) LEAP_CASE(64, 3) LEAP_CASE(64, 4) LEAP_CASE(64, 8)
     LEAP_CASE(128, 1) LEAP_CASE(128, 2) LEAP_CASE(128, 3) LEAP_CASE(128, 4) LEAP_CASE(128, 8)

@@ -2,5 +2,5 @@
 #include "kernels_decode_table.hpp"
 
 namespace leap_kernels {
-template KernelFn pick_decode<64, false>(int g, bool valu, bool kvs, int waves);
+template KernelFn pick_decode<64, false>(int g, bool valu, int kvs, int waves);
 }  // namespace leap_kernels

@@ -145,7 +145,7 @@ KvView kv_view(int group, int n_kv_heads)
 bool shape_supported(int head_dim, int group)
 {
     const KvView v = kv_view(group, 1);
-    return pick_kernel(head_dim, v.group, kDecode, false, false, v.kv_split != 0) != nullptr;
+    return pick_kernel(head_dim, v.group, kDecode, false, false, v.kv_split) != nullptr;
 }
 
 int check_layer(leap_hip_attention *h, int layer)
@@ -199,7 +199,7 @@ LaunchShape shape_of(const leap_hip_attention *h)
 
 // Small launches of 4 or 8 q heads per KV head, over at most kXcds
 // (sequence, KV head) groups, run as two launch groups of 2 or 4 q heads per
-// cache head (kv_split, instances of their own): each workgroup reads its
+// cache head (kv_split 1, instances of their own): each workgroup reads its
 // chunk's rows for half the heads, so the launch has twice the workgroups,
 // each with half the score, softmax, combine and fold work.  Same process,
 // both orders, graph replay, µs per layer-step, 8 q heads per KV head (up to
@@ -213,15 +213,32 @@ LaunchShape shape_of(const leap_hip_attention *h)
 // 70B heads at ctx 4096 (32 MiB) 11.67 -> 12.30, TinyLlama at 32768 23.1 ->
 // 26.1, one KV head at 32768 16.8 -> 18.3, Llama-3-8B heads at ctx 2048 (16
 // MiB) 6.81 -> 8.09.
+// The smallest launches of 8 q heads per KV head over four (sequence, KV
+// head) groups (up to 2 MiB) go one step further, four launch groups of 2 q
+// heads per cache head (sixteen groups, two per XCD), against twins:
+// TinyLlama ctx 1 3.57 -> 3.21, 64 3.64 -> 3.33, 256 4.86-4.99 -> 4.69-4.74,
+// 512 5.06-5.10 -> 4.76-4.82, 1024 (2 MiB) 5.49-5.52 either way; 4 KV heads
+// of 8 at head_dim 128 ctx 512 5.62 -> 5.22, 1024 (4 MiB) 6.12 -> 5.89, but
+// TinyLlama ctx 2048 (4 MiB) 6.06 -> 7.03.  With one group (one KV head)
+// they lost: ctx 2048 (2 MiB) 6.31 -> 6.92, 4096 9.03 -> 9.47.
 long long twin_bytes(int group)
 {
     return group == 8 ? 24ll << 20 : group == 4 ? 8ll << 20 : -1;
 }
+constexpr long long kQuarterBytes = 2ll << 20;
 LaunchShape launch_view(const LaunchShape &s, int n_seq, long long total_rows)
 {
     LaunchShape v = s;
+    const long long bytes = total_rows * s.n_kv_heads * s.head_dim * 8ll;
+    if (s.group == 8 && s.kv_split == 0 && !s.valu && (long long)n_seq * s.n_kv_heads == leap::kXcds / 2 &&
+        bytes <= kQuarterBytes) {
+        v.group = 2;
+        v.n_kv_heads = 4 * s.n_kv_heads;
+        v.kv_split = 2;
+        return v;
+    }
     if (s.kv_split == 0 && !s.valu && (long long)n_seq * s.n_kv_heads <= leap::kXcds &&
-        total_rows * s.n_kv_heads * s.head_dim * 8ll <= twin_bytes(s.group)) {
+        bytes <= twin_bytes(s.group)) {
         v.group = s.group / 2;
         v.n_kv_heads = 2 * s.n_kv_heads;
         v.kv_split = 1;
@@ -433,7 +450,7 @@ hipError_t launch_attention(const LaunchShape &shape, const LaunchBuffers &b, in
     // passes, whose pass order it rotates (the 2-wave instances are all PART).
     const bool part =
         waves == kWavesShort || leap::part_launch(even, chunk, leap::rows_per_pass(hd, s.group, kWaves));
-    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split != 0, waves);
+    KernelFn fn = pick_kernel(hd, s.group, kind, s.valu, part, s.kv_split, waves);
     if (!fn) return hipErrorInvalidValue;
     const int n_chunk_max = even ? std::min(even, max_pos + 1) : (max_pos + 1 + chunk - 1) / chunk;  // chunks of the longest sequence
     if (n_chunk_max > s.max_chunks || s.n_kv_heads >= 65536) return hipErrorInvalidValue;  // (leap::Preload::w0)
@@ -840,8 +857,9 @@ int leap_hip_attention_create(const leap_hip_attention_config *cfg, leap_hip_att
     const size_t ws_rows = n_pg * kvv.group * leap::records_per_head(h->max_chunks);
     CREATE_TRY(hipMalloc(&h->ws_o, ws_rows * c.head_dim * sizeof(float)));
     CREATE_TRY(hipMalloc(&h->ws_ml, ws_rows * sizeof(float2)));
-    // (launch_view's two groups of 2 or 4 q heads per cache head: up to 2
-    // kXcds groups, whose records fit in those of kXcds groups of 4 or 8)
+    // (launch_view's two groups of 2 or 4 q heads per cache head, or four of
+    // 2: up to 2 kXcds groups, whose records fit in those of kXcds groups of
+    // 4 or 8)
     const bool twins = (kvv.group == 8 || kvv.group == 4) && kvv.kv_split == 0;
     const size_t n_ctr = std::max<size_t>(n_pg, twins ? 2 * leap::kXcds : 0);
     h->counter_bytes = n_ctr * leap::counters_per_group(h->max_chunks) * sizeof(int);

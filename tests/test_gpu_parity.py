@@ -307,10 +307,14 @@ def test_batched_small_ragged_with_tiny_contexts(split):
     # batches: up to 8 (sequence, KV head) groups
     (32, 4, 64, [700, 33]), (32, 4, 64, [700, 33, 1]), (32, 8, 128, [40]), (32, 8, 128, [40, 40]),
     (16, 2, 128, [3000, 17, 2, 1]), (16, 2, 128, [3000, 17, 2, 1, 64]),
+    # 8 q heads per KV head as four launch groups of 2: up to 2 MiB over four
+    # groups (TinyLlama: 1024 positions; one KV head: 4 sequences)
+    (32, 4, 64, [1024]), (32, 4, 64, [1025]), (32, 4, 64, [1]), (8, 1, 128, [2048]),
+    (8, 1, 128, [500, 3, 1, 64]), (8, 1, 128, [500, 3, 1, 64, 2]), (16, 2, 64, [300, 9]), (16, 2, 64, [300]),
 ])
 def test_twin_launch_group_limits(nh, nkv, hd, Ts):
-    """Launches on either side of the twin launch groups' limits (K/V bytes,
-    groups per launch), single and batched, against the oracle."""
+    """Launches on either side of the twin and quarter launch groups' limits
+    (K/V bytes, groups per launch), single and batched, against the oracle."""
     theta = 10000.0 if hd == 64 else 500000.0
     Ts = np.array(Ts)
     S = len(Ts)

@@ -29,7 +29,7 @@ def _ring(lib):
     (32, 8, 128, 4096, 512),  # 64 one-pass chunks per KV head: the asymmetric merge with the fold helper
     (24, 8, 128, 1000, 128),  # 16 chunks per KV head: the one-level merge
     (8, 4, 64, 50, 8),        # one chunk per KV head: the output written directly (4 of 8 workgroups idle)
-    (32, 4, 64, 50, 8),       # 8 q heads per KV head: two launch groups of 4 per cache head, none idle
+    (32, 4, 64, 50, 16),      # 8 q heads per KV head: four launch groups of 2 per cache head, 16 workgroups
 ])
 def test_timeline_build_matches_and_stamps_in_order(hip_device, nh, nkv, hd, T, n_wg):
     import torch
@@ -59,9 +59,14 @@ def test_timeline_build_matches_and_stamps_in_order(hip_device, nh, nkv, hd, T, 
     assert (t[:, START] > 0).all() and (t[:, END] >= t[:, START]).all()
     assert (ring[(launches - 1) % SLOTS, n_wg:, START] == 0).all()  # no workgroup beyond the grid
     # launch groups: small launches run 4 or 8 q heads per KV head as two
-    # groups of 2 or 4 per cache head (up to 8 and 24 MiB of K/V rows)
+    # groups of 2 or 4 per cache head (up to 8 and 24 MiB of K/V rows), 8 as
+    # four groups of 2 (up to 2 MiB over four groups)
     limit = {4: 8 << 20, 8: 24 << 20}.get(nh // nkv, -1)
-    groups = 2 * nkv if T * nkv * hd * 8 <= limit else nkv
+    kv_bytes = T * nkv * hd * 8
+    if nh // nkv == 8 and nkv == 4 and kv_bytes <= 2 << 20:
+        groups = 4 * nkv
+    else:
+        groups = 2 * nkv if kv_bytes <= limit else nkv
     # workgroup ids equal modulo 8 are one KV head's chunks; ids of the
     # missing heads (fewer than 8) leave at once
     idle = (np.arange(n_wg) % 8) >= groups
