@@ -1484,7 +1484,7 @@ int leap_hip_attention_floor_async(leap_hip_attention *h, int kind, int layer, i
         HIP_TRY(h, hipSetDevice(h->cfg.device));
         return launch_block_floor(h, layer, max_pos, (hipStream_t)stream);
     }
-    if (spreads(shape_of(h), n_seq, total_rows))
+    if (spreads(launch_view(shape_of(h), n_seq, total_rows), n_seq, total_rows))
         return set_err(h, -EINVAL,
                        "%d sequences of %d KV heads and %lld rows spread over the XCDs in the step; the floor "
                        "kernels have no spread grid",

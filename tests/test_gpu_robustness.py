@@ -133,6 +133,12 @@ def test_floor_launches_write_nothing(kind):
         with pytest.raises(LeapError) as ei:
             att.floor_async(kind, 0, 1, 8191, 8192, s.cuda_stream)
         assert "spread" in str(ei.value)
+    # four KV heads of 8 q heads at 24 MiB: as 4 groups the step would spread,
+    # as the 8 twin launch groups it runs it does not, and the floor follows
+    with HipAttention(32, 4, 64, 12288) as att:
+        s = torch.cuda.Stream()
+        att.floor_async(kind, 0, 1, 12287, 12288, s.cuda_stream)
+        s.synchronize()
         s.synchronize()
 
 
