@@ -147,7 +147,8 @@ int leap_hip_attention_kv_download(leap_hip_attention *h, int seq, int layer, in
  * a 4 MiB static device array, one per device (held until the process ends):
  * a fixed 144 KiB region of arrival counters for at most 128 launch groups
  * (128 KV heads, or 64 with 16 q heads per KV head, whose heads run as two
- * groups each) and 33 KiB of part records, then n_heads x 72 partial
+ * groups each; small launches of 4 or 8 q heads per KV head run as up to 16
+ * groups of 2 or 4 q heads) and 33 KiB of part records, then n_heads x 72 partial
  * records of (head_dim + 2) floats (for at least 8 KV heads' worth of q
  * heads), at most 64 split-K chunks per call (up to 107 heads of 128 or 211
  * heads of 64; Llama-3-8B uses 1.38 MB, Llama-3-70B 2.58 MB); larger shapes

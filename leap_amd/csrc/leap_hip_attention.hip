@@ -169,7 +169,7 @@ struct LaunchShape {
     bool valu = false;  // products as VALU FMAs instead of MFMAs (the A/B knob)
     bool ws_parts = true;  // the buffers hold part records and kXcds part-groups' records
     int fold_helper = 1;   // leap_hip_attention_set_fold_helper
-    int kv_split = 0;      // group and n_kv_heads are kv_view's (two launch groups per cache head)
+    int kv_split = 0;      // 2^kv_split launch groups per cache head (kv_view's, launch_view's)
 };
 
 // The device buffers of one launch (one layer): the cache slabs of sequence
