@@ -34,6 +34,8 @@ def _capture(fn, stream):
     (32, 8, 128, 3100, 2999, (2999, 17, 1200)),    # near-equal chunks of one pass, asymmetric merge
     (32, 8, 128, 8200, 8191, (8191, 8000, 300)),   # 128-row chunks of two passes, rotated
     (8, 1, 128, 20000, 19999, (19999, 5000, 40)),  # one KV head spread over the XCDs: two launches per step
+    (32, 4, 64, 600, 255, (255, 40, 500)),         # TinyLlama's heads as four launch groups of 2 (the batch: 12 groups)
+    (32, 8, 128, 1100, 1000, (1000, 3, 700)),      # Llama-3-8B's heads as two launch groups of 2
 ])
 def test_step_loop_replays_match_eager(hip_device, nh, nkv, hd, sl, pos, poss):
     """Four layers of single-sequence steps (split-K merge over several
