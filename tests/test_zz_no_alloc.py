@@ -28,7 +28,7 @@ def _packed_rope(att, torch):
 
 @pytest.mark.parametrize("nh,nkv,hd,seq_len,theta,positions", [
     (32, 8, 128, 4096, 500000.0, (4095, 1000)),   # Llama-3-8B: 64 chunks (asymmetric merge), then 16
-    (32, 4, 64, 512, 10000.0, (255, 40, 20)),      # TinyLlama: 8 half-pass chunks on 2-wave workgroups, one 4-wave chunk, one 2-wave chunk
+    (32, 4, 64, 512, 10000.0, (255, 40, 20)),      # TinyLlama as four launch groups of 2 q heads per KV head: 8 half-pass chunks on 2-wave workgroups, then one chunk each
     (32, 2, 128, 4096, 500000.0, (4095, 700)),     # 16 q heads per KV head: four groups of 8, spread over the XCDs
     (64, 8, 128, 8192, 500000.0, (8191, 3000)),    # Llama-3-70B heads
 ])
